@@ -1,0 +1,613 @@
+// K3a / K3b: bidirectional attention on gfx950 bf16 MFMA.
+//
+// One kernel template serves both paths:
+//   * K3a (dense varlen, modes 0/1): a workgroup of 4 wavefronts owns 128
+//     "M rows" of one segment and one KV head and streams the segment's keys
+//     through LDS in tiles of 64; each wavefront owns 32 M rows.
+//   * K3b (generation block vs cached KV, mode 2): a workgroup owns 32 M
+//     rows; its 4 wavefronts split every 128-key tile (32 keys each) and are
+//     merged in LDS at the end; long key ranges are also split across
+//     workgroups (partials in a workspace, merged by attn_combine_kernel).
+//
+// "M rows" pack the Hq/Hkv query heads that share a KV head: M row m of a
+// segment is token m / g, query head hkv*g + m % g (g = Hq/Hkv), so every
+// K/V byte brought into LDS serves all g heads.
+//
+// Per wavefront and key block of 32 the math is
+//   S^T[32 keys x 32 rows] = K[32 x 128] . Q^T[128 x 32]   (8 x mfma 32x32x16)
+//   online softmax over keys (rows live in lanes: lane%32 = M row)
+//   O^T[128 x 32] += V^T[128 x 32 keys] . P^T[32 keys x 32] (8 x mfma 32x32x16)
+// Computing the transposed products keeps the softmax statistics and the
+// O^T accumulator of an M row in the same lane, so P^T goes straight from
+// the S^T accumulator registers into the B operand of the second product.
+// The key order inside each group of 16 is permuted consistently in the V^T
+// LDS tile and in P^T (a contraction is invariant under a permutation of its
+// summation index), which makes every operand fetch one 16-byte LDS read.
+#include "common.h"
+
+#include <math.h>
+
+namespace dllm {
+
+constexpr int HD = 128;       // head dim handled by this build
+constexpr int KSTR = HD + 8;  // LDS row stride (elements) of the K tile: 272 B, conflict-free 16 B reads
+
+template <int WM, int WK, int KBW>
+struct Cfg {
+  static constexpr int NKT = 32 * KBW * WK;  // keys per workgroup tile
+  static constexpr int VSTR = NKT + 8;       // LDS row stride (elements) of the V^T tile
+  static constexpr int K_ELEMS = NKT * KSTR;
+  static constexpr int V_ELEMS = HD * VSTR;
+  static constexpr int BUF_ELEMS = K_ELEMS + V_ELEMS;
+  static constexpr int BM = 32 * WM;               // M rows per workgroup
+  static constexpr int KCH = NKT / 16;             // 16-byte K chunks per thread per tile
+  static constexpr int VGR = NKT / 64;             // (4 keys x 8 d) V groups per thread per tile
+  static constexpr int LDS_BYTES = 2 * BUF_ELEMS * 2;
+};
+
+struct SegDesc {
+  int qrow0;     // first q / o row of the segment
+  int Lq;        // q rows (tokens)
+  int krow0;     // first contiguous k / v row
+  int Lkb;       // contiguous k / v rows
+  int n_c;       // cached rows in front of the contiguous ones (K3b)
+  int slot_base; // offset of this segment's slots
+};
+
+struct AttnArgs {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  uint16_t* o;
+  const uint16_t* k_cache;
+  const uint16_t* v_cache;
+  const int32_t* cu_q;
+  const int32_t* cu_k;
+  const int32_t* seg_ids;
+  const int32_t* slots;
+  const int32_t* slot_off;
+  float* ws;          // split partials (K3b, n_split > 1)
+  int64_t q_stride, k_stride, v_stride, o_stride;
+  int64_t cache_slots;
+  int n_seg, Hkv, g, mtiles, n_split, keys_per_split;
+  int logical_blocks;
+  float scale_log2;
+};
+
+__device__ __forceinline__ int xcd_remap(int b, int nb) {
+  // Work-groups are dispatched round-robin over the 8 XCDs; give each XCD a
+  // contiguous range of logical tiles so the tiles of one (segment, head),
+  // which read the same K/V, share that XCD's L2.
+  const int per = nb >> 3;
+  return (b & 7) * per + (b >> 3);
+}
+
+// Address of key/value row `kidx` of a segment for KV head hkv (nullptr: zero row).
+template <bool CACHED>
+__device__ __forceinline__ const uint16_t* kv_row(const uint16_t* base, const uint16_t* cache, int64_t stride,
+                                                  const AttnArgs& a, const SegDesc& sd, int hkv, int kidx) {
+  if (CACHED && kidx < sd.n_c) {
+    const int64_t s = a.slots[sd.slot_base + kidx];
+    if (s < 0 || s >= a.cache_slots) return nullptr;
+    return cache + s * (int64_t)(a.Hkv * HD) + hkv * HD;
+  }
+  return base + (int64_t)(sd.krow0 + kidx - (CACHED ? sd.n_c : 0)) * stride + hkv * HD;
+}
+
+template <int WM, int WK, int KBW, bool CACHED>
+struct TileIO {
+  using C = Cfg<WM, WK, KBW>;
+  u32x4_t kr[C::KCH];
+  u32x4_t vr[C::VGR][4];
+
+  __device__ __forceinline__ void load(const AttnArgs& a, const SegDesc& sd, int hkv, int k0, int kend) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < C::KCH; ++i) {
+      const int row = (tid >> 4) + 16 * i;
+      const int ch = tid & 15;
+      const int kidx = k0 + row;
+      u32x4_t val = {0u, 0u, 0u, 0u};
+      if (kidx < kend) {
+        const uint16_t* p = kv_row<CACHED>(a.k, a.k_cache, a.k_stride, a, sd, hkv, kidx);
+        if (p) val = ld128(p + ch * 8);
+      }
+      kr[i] = val;
+    }
+#pragma unroll
+    for (int i = 0; i < C::VGR; ++i) {
+      const int idx = tid + 256 * i;
+      const int kg = idx % (C::NKT / 4);
+      const int dc = idx / (C::NKT / 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int kidx = k0 + kg * 4 + e;
+        u32x4_t val = {0u, 0u, 0u, 0u};
+        if (kidx < kend) {
+          const uint16_t* p = kv_row<CACHED>(a.v, a.v_cache, a.v_stride, a, sd, hkv, kidx);
+          if (p) val = ld128(p + dc * 8);
+        }
+        vr[i][e] = val;
+      }
+    }
+  }
+
+  __device__ __forceinline__ void store(uint16_t* buf) const {
+    const int tid = threadIdx.x;
+    uint16_t* Ks = buf;
+    uint16_t* Vt = buf + C::K_ELEMS;
+#pragma unroll
+    for (int i = 0; i < C::KCH; ++i) {
+      const int row = (tid >> 4) + 16 * i;
+      const int ch = tid & 15;
+      *reinterpret_cast<u32x4_t*>(Ks + row * KSTR + ch * 8) = kr[i];
+    }
+#pragma unroll
+    for (int i = 0; i < C::VGR; ++i) {
+      const int idx = tid + 256 * i;
+      const int kg = idx % (C::NKT / 4);
+      const int dc = idx / (C::NKT / 4);
+      const int j = kg & 3;
+      // Keys 4kg..4kg+3 sit at positions pos..pos+3 of the permuted order:
+      // inside a group of 16 keys, position 8h + i holds key 4h + (i%4) + 8(i/4).
+      const int pos = 16 * (kg >> 2) + 8 * (j & 1) + 4 * (j >> 1);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {  // word w holds d = dc*8 + 2w (low half), 2w+1 (high half)
+        const uint32_t a0 = vr[i][0][w], a1 = vr[i][1][w], a2 = vr[i][2][w], a3 = vr[i][3][w];
+        u32x2_t lo, hi;
+        lo[0] = (a0 & 0xffffu) | (a1 << 16);
+        lo[1] = (a2 & 0xffffu) | (a3 << 16);
+        hi[0] = (a0 >> 16) | (a1 & 0xffff0000u);
+        hi[1] = (a2 >> 16) | (a3 & 0xffff0000u);
+        const int d = dc * 8 + 2 * w;
+        *reinterpret_cast<u32x2_t*>(Vt + d * C::VSTR + pos) = lo;
+        *reinterpret_cast<u32x2_t*>(Vt + (d + 1) * C::VSTR + pos) = hi;
+      }
+    }
+  }
+};
+
+template <int WM, int WK, int KBW, bool CACHED>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WK == 1 ? 2 : 1, WK == 1 ? 2 : 1))) void attn_fwd_kernel(AttnArgs a) {
+  using C = Cfg<WM, WK, KBW>;
+  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+
+  const int L = xcd_remap(blockIdx.x, gridDim.x);
+  if (L >= a.logical_blocks) return;
+
+  int r = L;
+  int split = 0;
+  if (CACHED) {
+    split = r % a.n_split;
+    r /= a.n_split;
+  }
+  const int mt = r % a.mtiles;
+  r /= a.mtiles;
+  const int hkv = r % a.Hkv;
+  const int s = r / a.Hkv;
+  const int sid = a.seg_ids ? a.seg_ids[s] : s;
+
+  SegDesc sd;
+  sd.qrow0 = a.cu_q[sid];
+  sd.Lq = a.cu_q[sid + 1] - sd.qrow0;
+  if (CACHED) {
+    sd.krow0 = sd.qrow0;
+    sd.Lkb = sd.Lq;
+    sd.slot_base = a.slot_off[s];
+    sd.n_c = a.slot_off[s + 1] - sd.slot_base;
+  } else {
+    sd.krow0 = a.cu_k[sid];
+    sd.Lkb = a.cu_k[sid + 1] - sd.krow0;
+    sd.n_c = 0;
+    sd.slot_base = 0;
+  }
+  const int g = a.g;
+  const int M = sd.Lq * g;
+  const int m_base = mt * C::BM;
+  if (m_base >= M) return;
+  const int Lk = sd.n_c + sd.Lkb;
+  int kbeg = 0, kend = Lk;
+  if (CACHED) {
+    kbeg = split * a.keys_per_split;
+    kend = min(Lk, kbeg + a.keys_per_split);
+    if (kbeg > kend) kbeg = kend;
+  }
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int lrow = lane & 31;
+  const int hl = lane >> 5;
+  const int wm = wave % WM;
+  const int wk = wave / WM;
+
+  // ---- Q^T fragments (B operand of S^T = K Q^T), resident for the whole loop.
+  const int m = m_base + wm * 32 + lrow;
+  const bool m_ok = m < M;
+  const int tok = m_ok ? m / g : 0;
+  const int head = hkv * g + (m_ok ? m - tok * g : 0);
+  bf16x8_t qf[8];
+  {
+    const uint16_t* qp = a.q + (int64_t)(sd.qrow0 + tok) * a.q_stride + head * HD + hl * 8;
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
+      u32x4_t t = {0u, 0u, 0u, 0u};
+      if (m_ok) t = ld128(qp + kk * 16);
+      qf[kk] = as_bf16x8(t);
+    }
+  }
+
+  f32x16_t oacc[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) oacc[db][i] = 0.f;
+  float m_run = -INFINITY;
+  float l_run = 0.f;  // this lane's half of the row sum
+
+  const int ntiles = (kend - kbeg + C::NKT - 1) / C::NKT;
+  TileIO<WM, WK, KBW, CACHED> io;
+  if (ntiles > 0) {
+    io.load(a, sd, hkv, kbeg, kend);
+    io.store(smem);
+  }
+  __syncthreads();
+
+  for (int t = 0; t < ntiles; ++t) {
+    const int k0 = kbeg + t * C::NKT;
+    const bool more = t + 1 < ntiles;
+    if (more) io.load(a, sd, hkv, k0 + C::NKT, kend);
+
+    const uint16_t* Ks = smem + (t & 1) * C::BUF_ELEMS;
+    const uint16_t* Vt = Ks + C::K_ELEMS;
+
+    // ---- S^T for this wavefront's key blocks
+    f32x16_t sacc[KBW];
+#pragma unroll
+    for (int b = 0; b < KBW; ++b) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) sacc[b][i] = 0.f;
+      const int kb = wk * KBW + b;
+      const uint16_t* kp = Ks + (kb * 32 + lrow) * KSTR + hl * 8;
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) {
+        const bf16x8_t af = as_bf16x8(*reinterpret_cast<const u32x4_t*>(kp + kk * 16));
+        sacc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, qf[kk], sacc[b], 0, 0, 0);
+      }
+    }
+
+    // ---- online softmax (log2 domain)
+    const bool tail = k0 + C::NKT > kend;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int b = 0; b < KBW; ++b) {
+      const int kb = wk * KBW + b;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        float x = sacc[b][i] * a.scale_log2;
+        if (tail) {
+          const int key = k0 + kb * 32 + 8 * (i >> 2) + 4 * hl + (i & 3);
+          if (key >= kend) x = -INFINITY;
+        }
+        sacc[b][i] = x;
+        mx = fmaxf(mx, x);
+      }
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float m_new = fmaxf(m_run, mx);
+    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+    float psum = 0.f;
+    bf16x8_t pf[2 * KBW];
+#pragma unroll
+    for (int b = 0; b < KBW; ++b) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        u32x4_t pk;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const float p0 = __builtin_amdgcn_exp2f(sacc[b][8 * j + 2 * w] - m_use);
+          const float p1 = __builtin_amdgcn_exp2f(sacc[b][8 * j + 2 * w + 1] - m_use);
+          psum += p0 + p1;
+          pk[w] = pack_bf16x2(p0, p1);
+        }
+        pf[2 * b + j] = as_bf16x8(pk);
+      }
+    }
+    l_run = l_run * alpha + psum;
+    m_run = m_new;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) oacc[db][i] *= alpha;
+
+    // ---- O^T += V^T P^T
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      const uint16_t* vp = Vt + (db * 32 + lrow) * C::VSTR + wk * KBW * 32 + hl * 8;
+#pragma unroll
+      for (int c = 0; c < 2 * KBW; ++c) {
+        const bf16x8_t af = as_bf16x8(*reinterpret_cast<const u32x4_t*>(vp + c * 16));
+        oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, pf[c], oacc[db], 0, 0, 0);
+      }
+    }
+
+    if (more) io.store(smem + ((t + 1) & 1) * C::BUF_ELEMS);
+    __syncthreads();
+  }
+
+  const float l_tot = l_run + __shfl_xor(l_run, 32);
+
+  if constexpr (WK == 1) {
+    // ---- direct epilogue: normalise and store bf16
+    if (m_ok) {
+      const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+      uint16_t* op = a.o + (int64_t)(sd.qrow0 + tok) * a.o_stride + head * HD;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int rq = 0; rq < 4; ++rq) {
+          const int d = db * 32 + 8 * rq + 4 * hl;
+          u32x2_t w;
+          w[0] = pack_bf16x2(oacc[db][4 * rq + 0] * inv, oacc[db][4 * rq + 1] * inv);
+          w[1] = pack_bf16x2(oacc[db][4 * rq + 2] * inv, oacc[db][4 * rq + 3] * inv);
+          *reinterpret_cast<u32x2_t*>(op + d) = w;
+        }
+    }
+  } else {
+    // ---- merge the WK wavefronts' partial softmax states in LDS
+    float* red = reinterpret_cast<float*>(smem);
+    float* red_m = red;                 // [WK][32]
+    float* red_l = red + WK * 32;       // [WK][32]
+    float* ored = red + 2 * WK * 32;    // [WK][128][32]
+    if (hl == 0) {
+      red_m[wk * 32 + lrow] = m_run;
+      red_l[wk * 32 + lrow] = l_tot;
+    }
+    __syncthreads();
+    float m_all = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < WK; ++w) m_all = fmaxf(m_all, red_m[w * 32 + lrow]);
+    const float m_all_use = (m_all == -INFINITY) ? 0.f : m_all;
+    const float fac = __builtin_amdgcn_exp2f(m_run - m_all_use);
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int d = db * 32 + 8 * (i >> 2) + 4 * hl + (i & 3);
+        ored[(wk * HD + d) * 32 + lrow] = oacc[db][i] * fac;
+      }
+    __syncthreads();
+    // 256 threads: row q = tid / 8, 16 consecutive d per thread.
+    const int q = tid >> 3;
+    const int d0 = (tid & 7) * 16;
+    float mq = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < WK; ++w) mq = fmaxf(mq, red_m[w * 32 + q]);
+    const float mq_use = (mq == -INFINITY) ? 0.f : mq;
+    float lq = 0.f;
+#pragma unroll
+    for (int w = 0; w < WK; ++w) lq += red_l[w * 32 + q] * __builtin_amdgcn_exp2f(red_m[w * 32 + q] - mq_use);
+    float acc[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      float sum = 0.f;
+#pragma unroll
+      for (int w = 0; w < WK; ++w) sum += ored[(w * HD + d0 + i) * 32 + q];
+      acc[i] = sum;
+    }
+    const int mrow = m_base + q;
+    if (mrow < M) {
+      const int tq = mrow / g;
+      const int hq = hkv * g + (mrow - tq * g);
+      if (a.n_split == 1) {
+        const float inv = lq > 0.f ? 1.f / lq : 0.f;
+        uint16_t* op = a.o + (int64_t)(sd.qrow0 + tq) * a.o_stride + hq * HD + d0;
+        u32x4_t w0, w1;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          w0[w] = pack_bf16x2(acc[2 * w] * inv, acc[2 * w + 1] * inv);
+          w1[w] = pack_bf16x2(acc[8 + 2 * w] * inv, acc[8 + 2 * w + 1] * inv);
+        }
+        st128(op, w0);
+        st128(op + 8, w1);
+      } else {
+        // partial record P = ((s*Hkv + hkv)*mtiles + mt)*n_split + split, 32 rows each
+        const int64_t P = (((int64_t)s * a.Hkv + hkv) * a.mtiles + mt) * a.n_split + split;
+        float* po = a.ws + (P * 32 + q) * HD + d0;
+#pragma unroll
+        for (int i = 0; i < 16; i += 4) {
+          f32x4_t v4 = {acc[i], acc[i + 1], acc[i + 2], acc[i + 3]};
+          *reinterpret_cast<f32x4_t*>(po + i) = v4;
+        }
+        if ((tid & 7) == 0) {
+          const int64_t nrec = (int64_t)a.n_seg * a.Hkv * a.mtiles * a.n_split;
+          float* pml = a.ws + nrec * 32 * HD + (P * 32 + q) * 2;
+          pml[0] = mq;
+          pml[1] = lq;
+        }
+      }
+    }
+  }
+}
+
+// Merge the n_split partial records of every (segment, head, M row).
+// grid: (n_seg*Hkv*mtiles*32) rows / 2 per block; block 256 = 2 rows x 128 d.
+__global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
+  const int row_rec = blockIdx.x * 2 + (threadIdx.x >> 7);  // (s, hkv, mt, q) flattened
+  const int d = threadIdx.x & 127;
+  const int total_rows = a.n_seg * a.Hkv * a.mtiles * 32;
+  if (row_rec >= total_rows) return;
+  const int q = row_rec & 31;
+  int r = row_rec >> 5;
+  const int mt = r % a.mtiles;
+  r /= a.mtiles;
+  const int hkv = r % a.Hkv;
+  const int s = r / a.Hkv;
+  const int sid = a.seg_ids ? a.seg_ids[s] : s;
+  const int qrow0 = a.cu_q[sid];
+  const int Lq = a.cu_q[sid + 1] - qrow0;
+  const int g = a.g;
+  const int mrow = mt * 32 + q;
+  if (mrow >= Lq * g) return;
+  const int64_t nrec = (int64_t)a.n_seg * a.Hkv * a.mtiles * a.n_split;
+  const int64_t P0 = (((int64_t)s * a.Hkv + hkv) * a.mtiles + mt) * a.n_split;
+  const float* ml = a.ws + nrec * 32 * HD;
+  float mx = -INFINITY;
+  for (int sp = 0; sp < a.n_split; ++sp) mx = fmaxf(mx, ml[((P0 + sp) * 32 + q) * 2]);
+  const float mu = (mx == -INFINITY) ? 0.f : mx;
+  float l = 0.f, acc = 0.f;
+  for (int sp = 0; sp < a.n_split; ++sp) {
+    const float* rec = ml + ((P0 + sp) * 32 + q) * 2;
+    const float w = __builtin_amdgcn_exp2f(rec[0] - mu);
+    l += rec[1] * w;
+    acc += a.ws[((P0 + sp) * 32 + q) * HD + d] * w;
+  }
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  const int tq = mrow / g;
+  const int hq = hkv * g + (mrow - tq * g);
+  a.o[(int64_t)(qrow0 + tq) * a.o_stride + hq * HD + d] = (uint16_t)f32_to_bf16_bits(acc * inv);
+}
+
+static const float kLog2e = 1.4426950408889634f;
+
+// K3a: WM=4 wavefronts x 32 M rows, 64-key tiles (2 key blocks per wavefront).
+using DenseCfg = Cfg<4, 1, 2>;
+// K3b: 1 x 32 M rows, 128-key tiles split over 4 wavefronts.
+using CachedCfg = Cfg<1, 4, 1>;
+
+static int common_checks(const char* name, const void* q, const void* k, const void* v, const void* o, int Hq,
+                         int Hkv, int D, int64_t qs, int64_t ks, int64_t vs, int64_t os) {
+  if (D != HD) return fail(DLLM_ERR_UNSUPPORTED, "%s: head_dim %d not supported (this build handles 128)", name, D);
+  if (Hq <= 0 || Hkv <= 0 || Hq % Hkv != 0)
+    return fail(DLLM_ERR_INVALID_ARG, "%s: Hq=%d must be a positive multiple of Hkv=%d", name, Hq, Hkv);
+  if (!q || !k || !v || !o) return fail(DLLM_ERR_INVALID_ARG, "%s: null tensor pointer", name);
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
+    return fail(DLLM_ERR_INVALID_ARG, "%s: q/k/v/o must be 16-byte aligned", name);
+  if (qs % 8 || ks % 8 || vs % 8 || os % 8)
+    return fail(DLLM_ERR_INVALID_ARG, "%s: token strides must be multiples of 8 elements", name);
+  if (qs < (int64_t)Hq * D || os < (int64_t)Hq * D || ks < (int64_t)Hkv * D || vs < (int64_t)Hkv * D)
+    return fail(DLLM_ERR_INVALID_ARG, "%s: token stride smaller than a token row", name);
+  return DLLM_OK;
+}
+
+template <typename KernelFn>
+static int set_lds(KernelFn fn, int bytes, const char* name) {
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (e != hipSuccess) return fail(DLLM_ERR_HIP, "%s: hipFuncSetAttribute(LDS %d B): %s", name, bytes, hipGetErrorString(e));
+  return DLLM_OK;
+}
+
+}  // namespace dllm
+
+using namespace dllm;
+
+extern "C" int dllm_attn_varlen_fwd(const dllm_bf16* q, const dllm_bf16* k, const dllm_bf16* v, dllm_bf16* o,
+                                    const int32_t* cu_q, const int32_t* cu_k, const int32_t* seg_ids, int n_seg,
+                                    int max_seqlen_q, int Hq, int Hkv, int D, int64_t q_stride_tok,
+                                    int64_t k_stride_tok, int64_t v_stride_tok, int64_t o_stride_tok,
+                                    float softmax_scale, void* stream) {
+  const char* name = "dllm_attn_varlen_fwd";
+  int rc = common_checks(name, q, k, v, o, Hq, Hkv, D, q_stride_tok, k_stride_tok, v_stride_tok, o_stride_tok);
+  if (rc) return rc;
+  if (n_seg < 0 || max_seqlen_q < 0) return fail(DLLM_ERR_INVALID_ARG, "%s: negative n_seg / max_seqlen_q", name);
+  if (n_seg == 0 || max_seqlen_q == 0) return DLLM_OK;
+  if (!cu_q || !cu_k) return fail(DLLM_ERR_INVALID_ARG, "%s: null cu_seqlens", name);
+  AttnArgs a = {};
+  a.q = q; a.k = k; a.v = v; a.o = o;
+  a.cu_q = cu_q; a.cu_k = cu_k; a.seg_ids = seg_ids;
+  a.q_stride = q_stride_tok; a.k_stride = k_stride_tok; a.v_stride = v_stride_tok; a.o_stride = o_stride_tok;
+  a.n_seg = n_seg; a.Hkv = Hkv; a.g = Hq / Hkv;
+  a.mtiles = (int)(((int64_t)max_seqlen_q * a.g + DenseCfg::BM - 1) / DenseCfg::BM);
+  a.n_split = 1;
+  const int64_t logical = (int64_t)a.mtiles * Hkv * n_seg;
+  if (logical > (int64_t)1 << 30) return fail(DLLM_ERR_INVALID_ARG, "%s: problem too large", name);
+  a.logical_blocks = (int)logical;
+  a.scale_log2 = softmax_scale * kLog2e;
+  auto kern = attn_fwd_kernel<4, 1, 2, false>;
+  if ((rc = set_lds(kern, DenseCfg::LDS_BYTES, name))) return rc;
+  const int nb = (int)((logical + 7) / 8 * 8);
+  kern<<<dim3(nb), dim3(256), DenseCfg::LDS_BYTES, reinterpret_cast<hipStream_t>(stream)>>>(a);
+  return check_launch(name);
+}
+
+static int block_cached_plan(int n_seg, int max_q, int max_keys, int Hq, int Hkv, int& mtiles, int& n_split,
+                             int& keys_per_split) {
+  const int g = Hq / Hkv;
+  mtiles = (max_q * g + 31) / 32;
+  const int64_t pairs = (int64_t)n_seg * Hkv * mtiles;
+  // Aim for >= 2 workgroups per CU (256 CUs) with at least two 128-key tiles per split.
+  int64_t want = pairs > 0 ? (512 + pairs - 1) / pairs : 1;
+  const int max_split = max_keys > 0 ? (max_keys + 255) / 256 : 1;
+  if (want > max_split) want = max_split;
+  if (want < 1) want = 1;
+  n_split = (int)want;
+  const int tiles = (max_keys + CachedCfg::NKT - 1) / CachedCfg::NKT;
+  const int tiles_per_split = (tiles + n_split - 1) / n_split;
+  keys_per_split = tiles_per_split * CachedCfg::NKT;
+  if (keys_per_split <= 0) keys_per_split = CachedCfg::NKT;
+  n_split = max_keys > 0 ? (max_keys + keys_per_split - 1) / keys_per_split : 1;
+  return 0;
+}
+
+extern "C" size_t dllm_attn_block_cached_workspace_size(int n_seg, int max_q, int max_keys, int Hq, int Hkv, int D) {
+  (void)D;
+  if (n_seg <= 0 || max_q <= 0 || Hkv <= 0 || Hq <= 0 || Hq % Hkv) return 0;
+  int mtiles, n_split, kps;
+  block_cached_plan(n_seg, max_q, max_keys, Hq, Hkv, mtiles, n_split, kps);
+  if (n_split <= 1) return 0;
+  const size_t nrec = (size_t)n_seg * Hkv * mtiles * n_split;
+  return nrec * 32 * (HD + 2) * sizeof(float);
+}
+
+extern "C" int dllm_attn_block_cached_fwd(const dllm_bf16* q, const dllm_bf16* k, const dllm_bf16* v, dllm_bf16* o,
+                                          const int32_t* cu, const int32_t* seg_ids, int n_seg, int max_q,
+                                          int max_keys, const dllm_bf16* k_cache, const dllm_bf16* v_cache,
+                                          int64_t cache_slots, const int32_t* slots, const int32_t* slot_off,
+                                          int Hq, int Hkv, int D, int64_t q_stride_tok, int64_t k_stride_tok,
+                                          int64_t v_stride_tok, int64_t o_stride_tok, float softmax_scale,
+                                          void* workspace, size_t workspace_bytes, void* stream) {
+  const char* name = "dllm_attn_block_cached_fwd";
+  int rc = common_checks(name, q, k, v, o, Hq, Hkv, D, q_stride_tok, k_stride_tok, v_stride_tok, o_stride_tok);
+  if (rc) return rc;
+  if (n_seg < 0 || max_q < 0 || max_keys < 0) return fail(DLLM_ERR_INVALID_ARG, "%s: negative size", name);
+  if (n_seg == 0 || max_q == 0) return DLLM_OK;
+  if (!cu || !slot_off) return fail(DLLM_ERR_INVALID_ARG, "%s: null cu / slot_off", name);
+  if (cache_slots > 0 && (!k_cache || !v_cache || !slots))
+    return fail(DLLM_ERR_INVALID_ARG, "%s: null cache / slots", name);
+  if (cache_slots > 0 && (!aligned16(k_cache) || !aligned16(v_cache)))
+    return fail(DLLM_ERR_INVALID_ARG, "%s: caches must be 16-byte aligned", name);
+  AttnArgs a = {};
+  a.q = q; a.k = k; a.v = v; a.o = o;
+  a.k_cache = k_cache; a.v_cache = v_cache; a.cache_slots = cache_slots;
+  a.cu_q = cu; a.cu_k = cu; a.seg_ids = seg_ids; a.slots = slots; a.slot_off = slot_off;
+  a.q_stride = q_stride_tok; a.k_stride = k_stride_tok; a.v_stride = v_stride_tok; a.o_stride = o_stride_tok;
+  a.n_seg = n_seg; a.Hkv = Hkv; a.g = Hq / Hkv;
+  int mtiles, n_split, kps;
+  block_cached_plan(n_seg, max_q, max_keys, Hq, Hkv, mtiles, n_split, kps);
+  a.mtiles = mtiles; a.n_split = n_split; a.keys_per_split = kps;
+  if (n_split > 1) {
+    const size_t need = dllm_attn_block_cached_workspace_size(n_seg, max_q, max_keys, Hq, Hkv, D);
+    if (!workspace || workspace_bytes < need)
+      return fail(DLLM_ERR_WORKSPACE, "%s: workspace of %zu bytes needed, %zu given", name, need,
+                  workspace ? workspace_bytes : (size_t)0);
+    if (!aligned16(workspace)) return fail(DLLM_ERR_INVALID_ARG, "%s: workspace must be 16-byte aligned", name);
+    a.ws = reinterpret_cast<float*>(workspace);
+  }
+  const int64_t logical = (int64_t)n_split * mtiles * Hkv * n_seg;
+  if (logical > (int64_t)1 << 30) return fail(DLLM_ERR_INVALID_ARG, "%s: problem too large", name);
+  a.logical_blocks = (int)logical;
+  a.scale_log2 = softmax_scale * kLog2e;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  auto kern = attn_fwd_kernel<1, 4, 1, true>;
+  if ((rc = set_lds(kern, CachedCfg::LDS_BYTES, name))) return rc;
+  const int nb = (int)((logical + 7) / 8 * 8);
+  kern<<<dim3(nb), dim3(256), CachedCfg::LDS_BYTES, st>>>(a);
+  if ((rc = check_launch(name))) return rc;
+  if (n_split > 1) {
+    const int64_t rows = (int64_t)n_seg * Hkv * mtiles * 32;
+    attn_combine_kernel<<<dim3((unsigned)((rows + 1) / 2)), dim3(256), 0, st>>>(a);
+    if ((rc = check_launch(name))) return rc;
+  }
+  return DLLM_OK;
+}

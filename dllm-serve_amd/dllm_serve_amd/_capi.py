@@ -1,0 +1,181 @@
+"""ctypes binding of ``libdllm_attn.so`` (the gfx950 kernels behind the C ABI
+declared in ``include/dllm_attn.h``).
+
+The library is built in-tree by ``dllm-serve_amd/csrc/Makefile``.  ``torch``
+is imported before the library is loaded so that the library binds to the
+HIP runtime torch already loaded (both carry the soname libamdhip64.so.7):
+device pointers and streams are then shared.  There is no CPU fallback: when
+the library is missing every call raises ``RuntimeError``.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch  # noqa: F401  (must precede the library load, see module docstring)
+
+LIB_NAME = "libdllm_attn.so"
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+
+DLLM_OK = 0
+DLLM_ERR_INVALID_ARG = -1
+DLLM_ERR_UNSUPPORTED = -2
+DLLM_ERR_WORKSPACE = -3
+DLLM_ERR_HIP = -4
+
+# name -> (restype, argtypes); must match include/dllm_attn.h
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_I64 = ctypes.c_int64
+_F = ctypes.c_float
+_SZ = ctypes.c_size_t
+SIGNATURES = {
+    "dllm_last_error": (ctypes.c_char_p, []),
+    "dllm_abi_version": (_I, []),
+    "dllm_store_kvcache": (_I, [_P, _I64, _P, _I64, _P, _P, _I64, _P, _I, _I, _P]),
+    "dllm_load_kvcache": (_I, [_P, _I64, _P, _I64, _P, _P, _I64, _P, _I, _I, _P]),
+    "dllm_attn_varlen_fwd": (
+        _I,
+        [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I64, _I64, _I64, _I64, _F, _P],
+    ),
+    "dllm_attn_block_cached_workspace_size": (_SZ, [_I, _I, _I, _I, _I, _I]),
+    "dllm_attn_block_cached_fwd": (
+        _I,
+        [_P, _P, _P, _P, _P, _P, _I, _I, _I, _P, _P, _I64, _P, _P, _I, _I, _I,
+         _I64, _I64, _I64, _I64, _F, _P, _SZ, _P],
+    ),
+    "dllm_select_kv_workspace_size": (_SZ, [_I, _I, _I, _I, _I, _I]),
+    "dllm_select_kv_store": (
+        _I,
+        [_P, _P, _P, _I64, _I64, _I64, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _F,
+         _P, _P, _I64, _P, _P, _P, _SZ, _P],
+    ),
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+def load(path: str | None = None) -> ctypes.CDLL:
+    """Load (once) and return the library; raise RuntimeError if it is absent."""
+    global _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        p = path or LIB_PATH
+        if not os.path.exists(p):
+            raise RuntimeError(
+                f"{LIB_NAME} not found at {p}; build it with `make -C dllm-serve_amd/csrc` "
+                "(or __graft_entry__.build()). There is no CPU fallback for this path."
+            )
+        lib = ctypes.CDLL(p)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+        return lib
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != DLLM_OK:
+        msg = load().dllm_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what} failed (code {rc}): {msg}")
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _require_gpu(*tensors: torch.Tensor) -> None:
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError(
+                "dllm_serve_amd kernels run on the GPU only; got a tensor on "
+                f"{t.device} (there is no CPU fallback)"
+            )
+
+
+# ---------------------------------------------------------------- wrappers ---
+
+def store_kvcache(key, value, k_cache, v_cache, slot_mapping, n_tok, row_elems):
+    """K1: cache rows slot_mapping[i] <- key[i], value[i] (bit-exact)."""
+    _require_gpu(key, value, k_cache, v_cache, slot_mapping)
+    lib = load()
+    rc = lib.dllm_store_kvcache(
+        key.data_ptr(), key.stride(0), value.data_ptr(), value.stride(0),
+        k_cache.data_ptr(), v_cache.data_ptr(), k_cache.numel() // row_elems,
+        slot_mapping.data_ptr(), n_tok, row_elems, _stream(key.device))
+    _check(rc, "dllm_store_kvcache")
+
+
+def load_kvcache(key, value, k_cache, v_cache, slot_mapping, n_tok, row_elems):
+    """K2: key[i], value[i] <- cache rows slot_mapping[i] (bit-exact)."""
+    _require_gpu(key, value, k_cache, v_cache, slot_mapping)
+    lib = load()
+    rc = lib.dllm_load_kvcache(
+        key.data_ptr(), key.stride(0), value.data_ptr(), value.stride(0),
+        k_cache.data_ptr(), v_cache.data_ptr(), k_cache.numel() // row_elems,
+        slot_mapping.data_ptr(), n_tok, row_elems, _stream(key.device))
+    _check(rc, "dllm_load_kvcache")
+
+
+def attn_varlen_fwd(q, k, v, o, cu_q, cu_k, seg_ids, n_seg, max_seqlen_q, scale):
+    """K3a: bidirectional varlen attention of segments (q,k,v,o are [rows, H, D])."""
+    _require_gpu(q, k, v, o, cu_q, cu_k)
+    lib = load()
+    rc = lib.dllm_attn_varlen_fwd(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+        cu_q.data_ptr(), cu_k.data_ptr(), _ptr(seg_ids), n_seg, max_seqlen_q,
+        q.shape[1], k.shape[1], q.shape[2],
+        q.stride(0), k.stride(0), v.stride(0), o.stride(0), float(scale),
+        _stream(q.device))
+    _check(rc, "dllm_attn_varlen_fwd")
+
+
+def block_cached_workspace_size(n_seg, max_q, max_keys, Hq, Hkv, D) -> int:
+    return int(load().dllm_attn_block_cached_workspace_size(n_seg, max_q, max_keys, Hq, Hkv, D))
+
+
+def attn_block_cached_fwd(q, k, v, o, cu, seg_ids, n_seg, max_q, max_keys,
+                          k_cache, v_cache, slots, slot_off, scale, workspace):
+    """K3b: block rows attend to [cached rows (by slot) ; block rows]."""
+    _require_gpu(q, k, v, o, cu, slot_off)
+    lib = load()
+    Hkv, D = k.shape[1], k.shape[2]
+    cache_slots = k_cache.numel() // (Hkv * D) if k_cache is not None and k_cache.numel() else 0
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    rc = lib.dllm_attn_block_cached_fwd(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+        cu.data_ptr(), _ptr(seg_ids), n_seg, max_q, max_keys,
+        _ptr(k_cache) if cache_slots else None, _ptr(v_cache) if cache_slots else None,
+        cache_slots, _ptr(slots) if cache_slots else None, slot_off.data_ptr(),
+        q.shape[1], Hkv, D,
+        q.stride(0), k.stride(0), v.stride(0), o.stride(0), float(scale),
+        _ptr(workspace), ws_bytes, _stream(q.device))
+    _check(rc, "dllm_attn_block_cached_fwd")
+
+
+def select_workspace_size(n_job, max_kc, Hq, Hkv, D, head_select) -> int:
+    return int(load().dllm_select_kv_workspace_size(n_job, max_kc, Hq, Hkv, D, int(bool(head_select))))
+
+
+def select_kv_store(q, k, v, jobs, n_job, max_kc, max_keep, max_blk, head_select, pool_k,
+                    sqrt_d, k_cache, v_cache, slots, idx_out, workspace):
+    """K5/K6: selection + fused cache scatter (see include/dllm_attn.h)."""
+    _require_gpu(q, k, v, jobs, k_cache, v_cache, slots)
+    lib = load()
+    Hq, Hkv, D = q.shape[1], k.shape[1], q.shape[2]
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    rc = lib.dllm_select_kv_store(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), q.stride(0), k.stride(0), v.stride(0),
+        jobs.data_ptr(), n_job, max_kc, max_keep, max_blk, Hq, Hkv, D,
+        int(bool(head_select)), int(pool_k), float(sqrt_d),
+        k_cache.data_ptr(), v_cache.data_ptr(), k_cache.numel() // (Hkv * D),
+        slots.data_ptr(), _ptr(idx_out), _ptr(workspace), ws_bytes, _stream(q.device))
+    _check(rc, "dllm_select_kv_store")

@@ -1,0 +1,284 @@
+"""Drop-in ``Attention`` layer and KV-cache helpers on the gfx950 kernels.
+
+Interface of dllmserve/layers/attention.py (``Attention(num_heads,
+head_dim, scale, num_kv_heads, causal)``, ``.forward(q, k, v)``,
+``store_kvcache``, ``load_kvcache``, the ``k_cache`` / ``v_cache`` /
+``layer_id`` attributes a model runner binds).  The diffusion branch
+(attention.py:150-306) is reproduced per sequence:
+
+* cache state 0 or no SparseConfig: full bidirectional attention over the
+  sequence's rows (K3a);
+* state 1: full attention (K3a), and the top-n_keep non-block rows of every
+  KV head (``head_select``) or of all heads are written to the sequence's
+  cache slots (K5/K6 fused with K1);
+* state 2: the block rows attend to [cached rows ; block rows] (K3b), read
+  straight from the paged cache by slot, without the reference's gather and
+  concatenation copies.
+
+Per step the layer builds one launch plan from ``context.seqs`` (host
+integers only, no device synchronisation) and caches it on the Context, so
+the 32 layers of a forward reuse it.  Every kernel runs on the caller's
+current HIP stream; nothing falls back to the CPU.
+"""
+from __future__ import annotations
+
+import os
+
+import numpy as np
+import torch
+from torch import nn
+
+from .. import _capi
+from ..sparse.state import keep_count
+from ..utils.context import get_context
+
+
+def _check_rows(t: torch.Tensor, name: str) -> None:
+    if t.dim() != 3 or t.stride(-1) != 1 or t.stride(1) != t.shape[2]:
+        raise ValueError(f"{name} must be [rows, heads, head_dim] with contiguous heads; got shape "
+                         f"{tuple(t.shape)} strides {t.stride()}")
+
+
+def _slot_tensor(slot_mapping, device) -> torch.Tensor:
+    if not isinstance(slot_mapping, torch.Tensor):
+        slot_mapping = torch.tensor(list(slot_mapping), dtype=torch.int32)
+    if slot_mapping.dtype != torch.int32 or slot_mapping.device != device or not slot_mapping.is_contiguous():
+        slot_mapping = slot_mapping.to(device=device, dtype=torch.int32).contiguous()
+    return slot_mapping
+
+
+def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                  slot_mapping: torch.Tensor) -> None:
+    """k_cache.flat[slot_mapping[i], :] = key[i], same for value (attention.py:33-50)."""
+    N, num_heads, head_dim = key.shape
+    D = num_heads * head_dim
+    assert key.stride(-1) == 1 and value.stride(-1) == 1
+    assert key.stride(1) == head_dim and value.stride(1) == head_dim
+    assert k_cache.stride(1) == D and v_cache.stride(1) == D
+    if slot_mapping.numel() != N:
+        print(f"Warning: slot_mapping.numel {slot_mapping.numel()} != N {N}")
+    assert slot_mapping.numel() == N
+    assert k_cache.is_contiguous() and v_cache.is_contiguous(), "KV cache must be contiguous"
+    assert key.dtype == value.dtype == k_cache.dtype == v_cache.dtype == torch.bfloat16, "bf16 tensors expected"
+    slot = _slot_tensor(slot_mapping, key.device)
+    _capi.store_kvcache(key, value, k_cache, v_cache, slot, N, D)
+
+
+def load_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                 slot_mapping: torch.Tensor) -> None:
+    """key[i] = k_cache.flat[slot_mapping[i], :], same for value (attention.py:77-92)."""
+    N, num_heads, head_dim = key.shape
+    D = num_heads * head_dim
+    assert key.stride(-1) == 1 and value.stride(-1) == 1
+    assert key.stride(1) == head_dim and value.stride(1) == head_dim
+    assert k_cache.stride(1) == D and v_cache.stride(1) == D
+    assert slot_mapping.numel() == N
+    assert k_cache.is_contiguous() and v_cache.is_contiguous(), "KV cache must be contiguous"
+    assert key.dtype == value.dtype == k_cache.dtype == v_cache.dtype == torch.bfloat16, "bf16 tensors expected"
+    slot = _slot_tensor(slot_mapping, key.device)
+    _capi.load_kvcache(key, value, k_cache, v_cache, slot, N, D)
+
+
+class StepPlan:
+    """Launch tables of one diffusion forward (shared by all layers).
+
+    Built from host integers of ``context.seqs``; uploaded with one copy.
+    """
+
+    def __init__(self, context, device: torch.device, num_kv_heads: int, head_dim: int, num_heads: int):
+        seqs = context.seqs
+        if not seqs:
+            raise ValueError("diffusion context has no sequences")
+        self.device = device
+        rows, modes, spans, keeps = [], [], [], []
+        for seq in seqs:
+            st = seq.sparse_state
+            N = seq.num_tokens
+            if st is None or st.is_full_attention:
+                modes.append(0)
+                rows.append(N)
+                spans.append((0, 0))
+                keeps.append(0)
+            elif st.should_compute_cache:
+                bs, bl = st.block_span(seq.num_prompt_tokens, N)
+                bl = max(0, min(bl, N - bs)) if bs < N else 0
+                if bl == 0:
+                    raise ValueError(f"sequence {seq.seq_id}: cache state 1 with an empty block "
+                                     f"(block start {bs}, {N} tokens)")
+                modes.append(1)
+                rows.append(N)
+                spans.append((bs, bl))
+                keeps.append(keep_count(N - bl, st.retention_ratio))
+            elif st.should_reuse_cache:
+                bs, bl = st.block_span(seq.num_prompt_tokens, N)
+                modes.append(2)
+                rows.append(bl)
+                spans.append((bs, bl))
+                keeps.append(seq.current_sparse_token)
+            else:
+                modes.append(-1)  # unrecognised state: rows stay zero (outputs = zeros_like(q))
+                rows.append(N)
+                spans.append((0, 0))
+                keeps.append(0)
+        self.n_seq = len(seqs)
+        self.total_rows = int(sum(rows))
+        cu = np.zeros(self.n_seq + 1, dtype=np.int64)
+        cu[1:] = np.cumsum(rows)
+        self.any_skipped = any(m == -1 for m in modes)
+
+        dense = [i for i, m in enumerate(modes) if m in (0, 1)]
+        jobs_idx = [i for i, m in enumerate(modes) if m == 1]
+        cached = [i for i, m in enumerate(modes) if m == 2]
+        self.n_dense = len(dense)
+        self.max_q_dense = max((rows[i] for i in dense), default=0)
+
+        # slots of sparse sequences: state-2 sequences first (contiguous, so
+        # slot_off below brackets each of them), then state-1 sequences
+        slot_mapping = context.slot_mapping if context.slot_mapping is not None else []
+        slot_parts, slot_base = [], {}
+        off = 0
+        for i in cached + jobs_idx:
+            if i >= len(slot_mapping):
+                raise ValueError(f"context.slot_mapping has no entry for sequence index {i}")
+            sm = slot_mapping[i]
+            n = sm.numel() if isinstance(sm, torch.Tensor) else len(sm)
+            if n != keeps[i]:
+                print(f"Warning: slot_mapping.numel {n} != N {keeps[i]}")
+            assert n == keeps[i]
+            slot_base[i] = off
+            off += n
+            slot_parts.append(_slot_tensor(sm, device))
+        self.slots = torch.cat(slot_parts) if slot_parts else torch.zeros(1, dtype=torch.int32, device=device)
+
+        # selection jobs: row0, n_tok, blk_start, blk_len, n_keep, slot_off
+        self.n_job = len(jobs_idx)
+        jobs = np.zeros((max(1, self.n_job), 6), dtype=np.int64)
+        for r, i in enumerate(jobs_idx):
+            bs, bl = spans[i]
+            jobs[r] = (cu[i], rows[i], bs, bl, keeps[i], slot_base[i])
+        self.max_kc = max((rows[i] - spans[i][1] for i in jobs_idx), default=0)
+        self.max_keep = max((keeps[i] for i in jobs_idx), default=0)
+        self.max_blk = max((spans[i][1] for i in jobs_idx), default=0)
+
+        # cached (state 2) segments: slot offsets indexed by position in `cached`
+        self.n_cached = len(cached)
+        slot_off = np.zeros(self.n_cached + 1, dtype=np.int64)
+        for r, i in enumerate(cached):
+            slot_off[r] = slot_base[i]
+            slot_off[r + 1] = slot_base[i] + keeps[i]
+        self.max_q_cached = max((rows[i] for i in cached), default=0)
+        self.max_keys_cached = max((rows[i] + keeps[i] for i in cached), default=0)
+
+        # one host->device copy of every int32 table
+        parts = [cu, np.array(dense or [0]), np.array(cached or [0]), slot_off, jobs.reshape(-1)]
+        flat = np.concatenate([p.astype(np.int64) for p in parts])
+        if flat.size and (flat.max() >= 2**31 or flat.min() < -(2**31)):
+            raise ValueError("step tables exceed int32")
+        host = torch.from_numpy(flat.astype(np.int32))
+        dev = host.to(device, non_blocking=False)
+        o = 0
+        self.cu = dev[o:o + cu.size]; o += cu.size
+        self.dense_ids = dev[o:o + max(1, len(dense))]; o += max(1, len(dense))
+        self.cached_ids = dev[o:o + max(1, len(cached))]; o += max(1, len(cached))
+        self.slot_off = dev[o:o + slot_off.size]; o += slot_off.size
+        self.jobs = dev[o:o + jobs.size]
+
+        self.head_select = None
+        self.pool_k = None
+        for i in jobs_idx:
+            cfg = seqs[i].sparse_state.config
+            hs, pk = bool(cfg.head_select), int(cfg.pool_kernel)
+            if self.head_select is None:
+                self.head_select, self.pool_k = hs, pk
+            elif (hs, pk) != (self.head_select, self.pool_k):
+                raise NotImplementedError("sequences with different head_select / pool_kernel in one step")
+
+        self._ws = {}
+        self.last_idx = None
+
+    def workspace(self, key: str, nbytes: int) -> torch.Tensor | None:
+        if nbytes <= 0:
+            return None
+        t = self._ws.get(key)
+        if t is None or t.numel() < nbytes:
+            t = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
+            self._ws[key] = t
+        return t
+
+
+class Attention(nn.Module):
+    """Drop-in for dllmserve.layers.attention.Attention (attention.py:95-119)."""
+
+    keep_indices = os.environ.get("DLLM_KEEP_SELECT_INDICES", "0") == "1"
+
+    def __init__(self, num_heads, head_dim, scale, num_kv_heads, causal=True):
+        super().__init__()
+        self.num_heads = num_heads
+        self.head_dim = head_dim
+        self.scale = scale
+        self.num_kv_heads = num_kv_heads
+        self.causal = causal
+        self.k_cache = self.v_cache = torch.tensor([])
+        self.layer_id = None
+        self.last_select_indices = None
+
+    def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+        q = q.view(-1, self.num_heads, self.head_dim)
+        k = k.view(-1, self.num_kv_heads, self.head_dim)
+        v = v.view(-1, self.num_kv_heads, self.head_dim)
+        context = get_context()
+        if context.is_diffusion:
+            return self._mixed_sparse_dense_attention(q, k, v, context)
+        raise NotImplementedError(
+            "only the diffusion branch (context.is_diffusion=True) is provided; the autoregressive "
+            "prefill/decode branch of the reference is unused by diffusion models")
+
+    def _plan(self, context, device) -> StepPlan:
+        plan = getattr(context, "_dllm_plan", None)
+        if plan is None or plan.device != device:
+            plan = StepPlan(context, device, self.num_kv_heads, self.head_dim, self.num_heads)
+            context._dllm_plan = plan
+        return plan
+
+    def _mixed_sparse_dense_attention(self, q, k, v, context):
+        for t, n in ((q, "q"), (k, "k"), (v, "v")):
+            _check_rows(t, n)
+        if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
+            raise TypeError(f"bf16 q/k/v expected, got {q.dtype}/{k.dtype}/{v.dtype}")
+        if not q.is_cuda:
+            raise RuntimeError("Attention runs on the GPU only (no CPU fallback)")
+        plan = self._plan(context, q.device)
+        if q.shape[0] != plan.total_rows or k.shape[0] != plan.total_rows or v.shape[0] != plan.total_rows:
+            raise ValueError(f"q/k/v have {q.shape[0]}/{k.shape[0]}/{v.shape[0]} rows, the step's sequences "
+                             f"feed {plan.total_rows}")
+        o = torch.zeros_like(q) if plan.any_skipped else torch.empty_like(q)
+        Hq, Hkv, D = self.num_heads, self.num_kv_heads, self.head_dim
+
+        if plan.n_dense:
+            _capi.attn_varlen_fwd(q, k, v, o, plan.cu, plan.cu, plan.dense_ids, plan.n_dense,
+                                  plan.max_q_dense, self.scale)
+
+        if plan.n_job:
+            if not (self.k_cache.numel() and self.v_cache.numel()):
+                raise RuntimeError("cache state 1 needs k_cache/v_cache bound to this layer")
+            ws = plan.workspace("select", _capi.select_workspace_size(
+                plan.n_job, plan.max_kc, Hq, Hkv, D, plan.head_select))
+            n_sel = Hkv if plan.head_select else 1
+            idx = None
+            if self.keep_indices:
+                idx = torch.full((plan.n_job, n_sel, plan.max_keep), -1, dtype=torch.int64, device=q.device)
+            _capi.select_kv_store(q, k, v, plan.jobs, plan.n_job, plan.max_kc, plan.max_keep, plan.max_blk,
+                                  plan.head_select, plan.pool_k, np.float32(D ** 0.5),
+                                  self.k_cache, self.v_cache, plan.slots, idx, ws)
+            self.last_select_indices = idx
+
+        if plan.n_cached:
+            if not (self.k_cache.numel() and self.v_cache.numel()):
+                raise RuntimeError("cache state 2 needs k_cache/v_cache bound to this layer")
+            ws = plan.workspace("cached", _capi.block_cached_workspace_size(
+                plan.n_cached, plan.max_q_cached, plan.max_keys_cached, Hq, Hkv, D))
+            _capi.attn_block_cached_fwd(q, k, v, o, plan.cu, plan.cached_ids, plan.n_cached,
+                                        plan.max_q_cached, plan.max_keys_cached,
+                                        self.k_cache, self.v_cache, plan.slots, plan.slot_off,
+                                        self.scale, ws)
+        return o.view(-1, Hq * D)

@@ -1,0 +1,168 @@
+/*
+ * dllm_attn.h -- C ABI of the MI355X (gfx950) diffusion-LLM attention path.
+ *
+ * Every entry point is asynchronous on the HIP stream it is given (pass the
+ * caller's current stream, e.g. torch.cuda.current_stream().cuda_stream),
+ * takes raw device pointers, element strides and sizes, never allocates
+ * device memory and never throws.  Return value 0 means the work was
+ * enqueued; a negative DLLM_ERR_* code means nothing was launched and
+ * dllm_last_error() describes why (thread-local, valid until the next call
+ * on the same thread).
+ *
+ * Tensors are bfloat16 (raw 16-bit patterns, type dllm_bf16), row-major,
+ * innermost dimension contiguous.  "Rows" are tokens: q is [rows, Hq, D],
+ * k / v are [rows, Hkv, D]; *_stride_tok is the element distance between
+ * consecutive tokens (>= H*D).  Heads are contiguous inside a token row.
+ *
+ * Each declaration names the reference interface (chosen-ox/dLLM-Serve,
+ * file:line) whose behaviour it reproduces.
+ */
+#ifndef DLLM_ATTN_H
+#define DLLM_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef uint16_t dllm_bf16; /* bfloat16 bit pattern */
+
+#define DLLM_OK 0
+#define DLLM_ERR_INVALID_ARG (-1) /* shape / stride / alignment / size mismatch */
+#define DLLM_ERR_UNSUPPORTED (-2) /* valid request this build does not implement (e.g. head_dim != 128) */
+#define DLLM_ERR_WORKSPACE (-3)   /* workspace pointer missing or too small */
+#define DLLM_ERR_HIP (-4)         /* a HIP runtime call or kernel launch failed */
+
+/* Message for the last failing call on this thread ("" if none). */
+const char* dllm_last_error(void);
+
+/* ABI version of this library (major * 100 + minor). */
+int dllm_abi_version(void);
+
+/*
+ * K1 -- KV-cache scatter.  Replaces store_kvcache / store_kvcache_kernel
+ * (dllmserve/layers/attention.py:11-50).
+ *
+ * For i in [0, n_tok): k_cache[slot_mapping[i] * row_elems + e] = key[i * key_stride_tok + e]
+ * and the same for value / v_cache, e in [0, row_elems), row_elems = Hkv * D.
+ * The cache is viewed as flat rows of row_elems elements (its slot stride is
+ * row_elems), as the reference asserts at attention.py:44.  cache_slots is
+ * the number of rows the cache holds; a slot outside [0, cache_slots) is
+ * skipped instead of written out of bounds (the reference does not check).
+ * Bit-exact copy.
+ */
+int dllm_store_kvcache(const dllm_bf16* key, int64_t key_stride_tok,
+                       const dllm_bf16* value, int64_t value_stride_tok,
+                       dllm_bf16* k_cache, dllm_bf16* v_cache, int64_t cache_slots,
+                       const int32_t* slot_mapping, int n_tok, int row_elems,
+                       void* stream);
+
+/*
+ * K2 -- KV-cache gather.  Replaces load_kvcache / load_kvcache_kernel
+ * (dllmserve/layers/attention.py:53-92):  key[i] = k_cache[slot_mapping[i]],
+ * value[i] = v_cache[slot_mapping[i]].  Rows whose slot is outside
+ * [0, cache_slots) are left untouched.  Bit-exact copy.
+ */
+int dllm_load_kvcache(dllm_bf16* key, int64_t key_stride_tok,
+                      dllm_bf16* value, int64_t value_stride_tok,
+                      const dllm_bf16* k_cache, const dllm_bf16* v_cache, int64_t cache_slots,
+                      const int32_t* slot_mapping, int n_tok, int row_elems,
+                      void* stream);
+
+/*
+ * K3a -- non-causal (bidirectional) varlen attention over packed segments.
+ * Replaces flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k,
+ * max_seqlen_q, max_seqlen_k, softmax_scale, causal=False)
+ * (dllmserve/layers/attention.py:289-299, the mode-0/1 rows of
+ * _mixed_sparse_dense_attention, attention.py:168-187).
+ *
+ * Segment s covers q rows [cu_q[id], cu_q[id+1]) and k/v rows
+ * [cu_k[id], cu_k[id+1]) where id = seg_ids ? seg_ids[s] : s, s in [0, n_seg).
+ * seg_ids lets a caller run a subset of the sequences of one packed batch in
+ * place, without packing copies.  For every q row t of segment s and head h:
+ *   o[t, h] = sum_u softmax_u(scale * q[t, h] . k[u, h / (Hq/Hkv)]) v[u, h / (Hq/Hkv)]
+ * bf16 inputs, fp32 accumulation, bf16 output.  max_seqlen_q must bound every
+ * segment's q length (it sizes the grid, as in flash-attn).  D must be 128;
+ * Hq must be a multiple of Hkv.  Pointers must be 16-byte aligned and the
+ * token strides multiples of 8 elements.  Rows of o outside the segments are
+ * not written.
+ */
+int dllm_attn_varlen_fwd(const dllm_bf16* q, const dllm_bf16* k, const dllm_bf16* v, dllm_bf16* o,
+                         const int32_t* cu_q, const int32_t* cu_k, const int32_t* seg_ids,
+                         int n_seg, int max_seqlen_q, int Hq, int Hkv, int D,
+                         int64_t q_stride_tok, int64_t k_stride_tok, int64_t v_stride_tok,
+                         int64_t o_stride_tok, float softmax_scale, void* stream);
+
+/*
+ * K3b -- attention of the current generation block against cached KV plus
+ * the block itself (mode 2 / "reuse cache").  Replaces the load_kvcache +
+ * torch.cat + flash_attn_varlen_func sequence of
+ * dllmserve/layers/attention.py:235-265,289-299.
+ *
+ * Segment s (id = seg_ids ? seg_ids[s] : s) has q rows and block k/v rows
+ * [cu[id], cu[id+1]) (the block tokens only) and n_c = slot_off[s+1] -
+ * slot_off[s] cached rows whose cache slots are slots[slot_off[s] + r].
+ * Keys/values of segment s are [cache rows r = 0..n_c-1 ; block rows].
+ * The cache is [cache_slots, Hkv, D] with slot stride Hkv*D (flat rows, as
+ * store_kvcache writes it).  A slot outside [0, cache_slots) contributes a
+ * zero key/value row.  max_q bounds the block length of every segment.
+ * The work is split over the keys when there are few segments; the partial
+ * results go to `workspace`, whose size must be at least
+ * dllm_attn_block_cached_workspace_size(...) bytes (0 is valid when that
+ * function returns 0).
+ */
+size_t dllm_attn_block_cached_workspace_size(int n_seg, int max_q, int max_keys, int Hq, int Hkv, int D);
+int dllm_attn_block_cached_fwd(const dllm_bf16* q, const dllm_bf16* k, const dllm_bf16* v, dllm_bf16* o,
+                               const int32_t* cu, const int32_t* seg_ids, int n_seg, int max_q, int max_keys,
+                               const dllm_bf16* k_cache, const dllm_bf16* v_cache, int64_t cache_slots,
+                               const int32_t* slots, const int32_t* slot_off,
+                               int Hq, int Hkv, int D,
+                               int64_t q_stride_tok, int64_t k_stride_tok, int64_t v_stride_tok,
+                               int64_t o_stride_tok, float softmax_scale,
+                               void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * K5 / K6 -- sparse KV selection fused with the KV-cache scatter (mode 1 /
+ * "compute cache").  Replaces _select_important_head_kv (head_select != 0,
+ * dllmserve/layers/attention.py:344-413), _select_important_kv (head_select
+ * == 0, attention.py:308-342) and the store_kvcache call that follows them
+ * (attention.py:189-233).
+ *
+ * jobs is an int32 array [n_job][6]: {row0, n_tok, blk_start, blk_len,
+ * n_keep, slot_off}.  For job j the sequence occupies q/k/v rows
+ * [row0, row0+n_tok); the current block is rows [blk_start, blk_start+blk_len)
+ * of the sequence; the candidates are the other Kc = n_tok - blk_len rows in
+ * order (prefix, then suffix).  Per selection head (each KV head when
+ * head_select != 0, one shared head otherwise) the n_keep candidates with the
+ * highest pooled score are written, best first, to cache slots
+ * slots[slot_off + r], r in [0, n_keep).  Scoring rule (deterministic;
+ * bit-exact against the oracle):
+ *   qbar[h, d]  = bf16(f32(f64 sum_t q[blk_start+t, h, d], t ascending) / blk_len))
+ *   raw[g, j]   = bf16(f32(f64 sum_d qbar[h_g, d] * k[cand j, kv, d], d ascending))
+ *                 (head_select == 0: one sum over h ascending then d ascending,
+ *                  with kv = h / (Hq/Hkv))
+ *   score[j]    = bf16(f32(max_g raw[g, j]) / f32(sqrt(D)))   (IEEE division)
+ *   pooled[j]   = max of score over [j - pool_k/2, j - pool_k/2 + pool_k - 1]
+ *                 clipped to the candidates (no pooling when pool_k <= 1)
+ *   order: pooled descending, then candidate index ascending.
+ * idx_out (nullable) receives the selected candidate indices as int64
+ * [n_job][n_sel_heads][max_keep] (n_sel_heads = Hkv or 1; entries r >= n_keep
+ * of a job are not written).  Kc must be <= 8192.  workspace must hold
+ * dllm_select_kv_workspace_size(...) bytes.
+ */
+size_t dllm_select_kv_workspace_size(int n_job, int max_kc, int Hq, int Hkv, int D, int head_select);
+int dllm_select_kv_store(const dllm_bf16* q, const dllm_bf16* k, const dllm_bf16* v,
+                         int64_t q_stride_tok, int64_t k_stride_tok, int64_t v_stride_tok,
+                         const int32_t* jobs, int n_job, int max_kc, int max_keep, int max_blk,
+                         int Hq, int Hkv, int D, int head_select, int pool_k, float sqrt_d,
+                         dllm_bf16* k_cache, dllm_bf16* v_cache, int64_t cache_slots,
+                         const int32_t* slots, int64_t* idx_out,
+                         void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DLLM_ATTN_H */

@@ -1,0 +1,152 @@
+"""K3a (dense varlen bidirectional) and K3b (block vs cached KV) on the GPU vs
+the fp32 oracle.  Tolerance (bf16 output vs fp32 reference on the same bf16
+inputs): max-abs <= 2e-2 and mean-abs <= 2e-3 (helpers.MAX_ABS / MEAN_ABS)."""
+import numpy as np
+import pytest
+import torch
+
+from helpers import assert_attn_close, bits, to_np
+
+from oracle import attention as oatt
+from oracle import configs
+from dllm_serve_amd import _capi
+
+pytestmark = pytest.mark.gpu
+
+
+def _run_varlen(q, k, v, cu, dev, seg_ids=None, o_init=None):
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    o = torch.zeros_like(qd) if o_init is None else o_init.to(dev)
+    cud = cu.to(dev)
+    lens = (cu[1:] - cu[:-1]).tolist()
+    ids = None
+    n_seg = len(lens)
+    if seg_ids is not None:
+        ids = torch.tensor(seg_ids, dtype=torch.int32, device=dev)
+        n_seg = len(seg_ids)
+        lens = [lens[i] for i in seg_ids]
+    _capi.attn_varlen_fwd(qd, kd, vd, o, cud, cud, ids, n_seg, max(lens), q.shape[-1] ** -0.5)
+    torch.cuda.synchronize()
+    return o
+
+
+def test_c1_single_layer(dev):
+    """C1 shape (1 x 512 tokens, 32 heads x 128, RoPE'd), bf16 on the GPU."""
+    print("varlen C1 512x32x128", flush=True)
+    q, k, v, cu, scale = configs.c1_single_layer()
+    qb, kb, vb = q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16)
+    o = _run_varlen(qb, kb, vb, cu, dev)
+    ref = oatt.varlen(to_np(qb), to_np(kb), to_np(vb), cu.numpy(), cu.numpy(), scale, dtype=np.float32)
+    assert_attn_close(o, ref, "C1")
+
+
+@pytest.mark.parametrize("lens,Hq,Hkv", [
+    ([1, 7, 33, 64, 127, 128, 129, 300], 32, 32),     # ragged MHA, tails everywhere
+    ([384] * 4, 32, 32),                               # C2 dense step shape (4 of the 8 sequences)
+    ([200, 517, 1], 28, 4),                            # Dream GQA, g = 7
+    ([96, 160], 8, 2),                                 # g = 4
+    ([1000], 4, 4),
+])
+def test_varlen_ragged(dev, lens, Hq, Hkv):
+    print(f"varlen lens={lens} Hq={Hq} Hkv={Hkv}", flush=True)
+    q, k, v, cu = configs.packed_qkv(lens, Hq, Hkv, 128, seed=sum(lens))
+    o = _run_varlen(q, k, v, cu, dev)
+    ref = oatt.varlen(to_np(q), to_np(k), to_np(v), cu.numpy(), cu.numpy(), 128 ** -0.5, dtype=np.float32)
+    assert_attn_close(o, ref, f"lens={lens}")
+
+
+def test_varlen_subset_leaves_other_rows(dev):
+    """seg_ids runs only some segments in place; other rows keep their contents."""
+    print("varlen seg_ids subset", flush=True)
+    lens = [50, 70, 90, 30]
+    q, k, v, cu = configs.packed_qkv(lens, 16, 16, 128, seed=5)
+    sentinel = torch.full_like(q, 3.0)
+    o = _run_varlen(q, k, v, cu, dev, seg_ids=[1, 3], o_init=sentinel)
+    ref = oatt.varlen(to_np(q), to_np(k), to_np(v), cu.numpy(), cu.numpy(), 128 ** -0.5, dtype=np.float32,
+                      seg_ids=[1, 3])
+    cu_l = cu.tolist()
+    for s in (1, 3):
+        assert_attn_close(o[cu_l[s]:cu_l[s + 1]], ref[cu_l[s]:cu_l[s + 1]], f"seg {s}")
+    for s in (0, 2):
+        assert torch.all(o[cu_l[s]:cu_l[s + 1]].cpu() == 3.0)
+
+
+def test_varlen_strided_views(dev):
+    """q/k/v as column slices of one merged qkv projection (token stride > row)."""
+    print("varlen strided views", flush=True)
+    Hq, Hkv, D = 28, 4, 128
+    lens = [150, 260]
+    n = sum(lens)
+    g = torch.Generator().manual_seed(11)
+    qkv = torch.randn(n, (Hq + 2 * Hkv) * D, generator=g).to(torch.bfloat16).to(dev)
+    q = qkv[:, :Hq * D].view(n, Hq, D)
+    k = qkv[:, Hq * D:(Hq + Hkv) * D].view(n, Hkv, D)
+    v = qkv[:, (Hq + Hkv) * D:].view(n, Hkv, D)
+    cu = torch.tensor([0, lens[0], n], dtype=torch.int32)
+    o = torch.zeros(n, Hq, D, dtype=torch.bfloat16, device=dev)
+    _capi.attn_varlen_fwd(q, k, v, o, cu.to(dev), cu.to(dev), None, 2, max(lens), D ** -0.5)
+    torch.cuda.synchronize()
+    ref = oatt.varlen(to_np(q), to_np(k), to_np(v), cu.numpy(), cu.numpy(), D ** -0.5, dtype=np.float32)
+    assert_attn_close(o, ref, "strided")
+
+
+def test_varlen_bad_head_dim_raises(dev):
+    q = torch.zeros(8, 4, 64, dtype=torch.bfloat16, device=dev)
+    cu = torch.tensor([0, 8], dtype=torch.int32, device=dev)
+    with pytest.raises(RuntimeError, match="head_dim"):
+        _capi.attn_varlen_fwd(q, q, q, torch.empty_like(q), cu, cu, None, 1, 8, 0.125)
+
+
+def _cached_case(prefix, blk, Hq, Hkv, seed, page=256, extra_pages=3):
+    """Cache with shuffled pages; per sequence `prefix[i]` cached rows and a
+    block of `blk[i]` rows."""
+    g = torch.Generator().manual_seed(seed)
+    D = 128
+    pages_per = [-(-p // page) for p in prefix]
+    n_pages = sum(pages_per) + extra_pages
+    perm = torch.randperm(n_pages, generator=g).tolist()
+    kc = torch.randn(n_pages * page, Hkv, D, generator=g).to(torch.bfloat16)
+    vc = torch.randn(n_pages * page, Hkv, D, generator=g).to(torch.bfloat16)
+    slots, at = [], 0
+    for p, npg in zip(prefix, pages_per):
+        s = []
+        for j in range(npg):
+            pid = perm[at + j]
+            fill = page if j < npg - 1 else p - page * (npg - 1)
+            s.extend(range(pid * page, pid * page + fill))
+        at += npg
+        slots.append(s)
+    q, k, v, cu = configs.packed_qkv(blk, Hq, Hkv, D, seed=seed + 1)
+    return q, k, v, cu, kc, vc, slots
+
+
+@pytest.mark.parametrize("prefix,blk,Hq,Hkv", [
+    ([608, 608, 608, 608], [64, 64, 64, 64], 32, 32),     # C4 reuse step (n_keep 608, block 64)
+    ([2100, 3000, 4096], [32, 32, 32], 32, 32),            # C5-like long prefixes
+    ([5, 300], [32, 17], 28, 4),                           # Dream GQA, short block tail
+    ([0, 1], [8, 3], 8, 8),                                # empty / single cached row
+])
+def test_block_cached(dev, prefix, blk, Hq, Hkv):
+    print(f"block_cached prefix={prefix} blk={blk} Hq={Hq} Hkv={Hkv}", flush=True)
+    q, k, v, cu, kc, vc, slots = _cached_case(prefix, blk, Hq, Hkv, seed=sum(prefix) + 1)
+    D = 128
+    slot_off = [0]
+    for s in slots:
+        slot_off.append(slot_off[-1] + len(s))
+    flat_slots = torch.tensor([x for s in slots for x in s] or [0], dtype=torch.int32)
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    o = torch.zeros_like(qd)
+    max_keys = max(p + b for p, b in zip(prefix, blk))
+    ws_bytes = _capi.block_cached_workspace_size(len(blk), max(blk), max_keys, Hq, Hkv, D)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev) if ws_bytes else None
+    _capi.attn_block_cached_fwd(qd, kd, vd, o, cu.to(dev), None, len(blk), max(blk), max_keys,
+                                kc.to(dev), vc.to(dev), flat_slots.to(dev),
+                                torch.tensor(slot_off, dtype=torch.int32, device=dev), D ** -0.5, ws)
+    torch.cuda.synchronize()
+    kcn, vcn = to_np(kc), to_np(vc)
+    cul = cu.tolist()
+    qn, kn, vn = to_np(q), to_np(k), to_np(v)
+    for i in range(len(blk)):
+        r0, r1 = cul[i], cul[i + 1]
+        ref = oatt.block_cached(qn[r0:r1], kn[r0:r1], vn[r0:r1], kcn, vcn, slots[i], D ** -0.5, dtype=np.float32)
+        assert_attn_close(o[r0:r1], ref, f"seq {i}")

@@ -1,0 +1,324 @@
+"""Benchmark of the diffusion attention path on one MI355X.
+
+Headline workload (LLaDA-8B, B=8, prompt 256 + gen 128, bf16): one dense
+denoising step's attention = 32 layer calls of Attention.forward over 8
+packed sequences of 384 tokens (32 heads x 128), each layer with its own
+q/k/v resident in HBM.  `value` = attention TFLOP/s over the timed steps
+(FLOPs = 4 * sum Lq*Lk*Hq*D).  Extra fields report the other shapes of the
+path (Dream GQA varlen, head-sparse C4 full/reuse, long-prefix block-cached
+attention with the KV scatter) and the CPU oracle baseline.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "dllm-serve_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+import numpy as np  # noqa: E402
+import torch  # noqa: E402
+
+METRIC = "bidirectional attn TFLOP/s (% MFMA peak); denoise-step tokens/s, LLaDA-8B, 1 GPU"
+PEAK_BF16_TFLOPS = 2500.0
+PEAK_HBM_GBS = 8000.0
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+class Timer:
+    """HIP events on torch's current stream (the stream every kernel of the
+    path is launched on)."""
+
+    def __init__(self):
+        self.a = torch.cuda.Event(enable_timing=True)
+        self.b = torch.cuda.Event(enable_timing=True)
+
+    def start(self):
+        self.a.record()
+
+    def stop_ms(self) -> float:
+        self.b.record()
+        self.b.synchronize()
+        return self.a.elapsed_time(self.b)
+
+
+def make_layers(lens, Hq, Hkv, D, n_layers, dev, seed):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    n = int(sum(lens))
+    out = []
+    for _ in range(n_layers):
+        q = torch.randn(n, Hq, D, generator=g, device=dev, dtype=torch.bfloat16)
+        k = torch.randn(n, Hkv, D, generator=g, device=dev, dtype=torch.bfloat16)
+        v = torch.randn(n, Hkv, D, generator=g, device=dev, dtype=torch.bfloat16)
+        out.append((q, k, v))
+    return out
+
+
+def dense_context(lens, dev):
+    """Context of a dense diffusion step (no SparseConfig) as the runner sets it."""
+    from dllm_serve_amd.engine.sequence import Sequence, prepare_step
+
+    seqs = [Sequence([0] * (n - 0), 0, 126336, None, device=dev) for n in lens]
+    prepare_step(seqs, dev)
+
+
+def time_layer_calls(attn, layers, steps, warmup):
+    """Run `steps` timed steps, each = one Attention.forward per layer."""
+    for _ in range(warmup):
+        for q, k, v in layers:
+            attn(q, k, v)
+    torch.cuda.synchronize()
+    t = Timer()
+    t.start()
+    for _ in range(steps):
+        for q, k, v in layers:
+            attn(q, k, v)
+    ms = t.stop_ms()
+    torch.cuda.synchronize()
+    return ms / steps
+
+
+def time_kernel(fn, iters=50, warmup=5):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t = Timer()
+    t.start()
+    for _ in range(iters):
+        fn()
+    return t.stop_ms() / iters
+
+
+def bench_dense(lens, Hq, Hkv, D, n_layers, steps, warmup, dev, seed=0):
+    from oracle.configs import attention_bytes, attention_flops
+    from dllm_serve_amd import _capi
+    from dllm_serve_amd.layers.attention import Attention
+    from dllm_serve_amd.utils.context import get_context, reset_context
+
+    attn = Attention(Hq, D, D ** -0.5, Hkv, causal=False)
+    layers = make_layers(lens, Hq, Hkv, D, n_layers, dev, seed)
+    dense_context(lens, dev)
+    ms_step = time_layer_calls(attn, layers, steps, warmup)
+    flops_call = attention_flops(lens, lens, Hq, D)
+    bytes_call = attention_bytes(lens, lens, Hq, Hkv, D)
+    # per-launch kernel time: the raw varlen kernel over distinct layers' buffers
+    plan = get_context()._dllm_plan
+    outs = [torch.empty_like(q) for q, _, _ in layers]
+    state = {"i": 0}
+
+    def one():
+        i = state["i"] % n_layers
+        state["i"] += 1
+        q, k, v = layers[i]
+        _capi.attn_varlen_fwd(q, k, v, outs[i], plan.cu, plan.cu, None, len(lens), max(lens), D ** -0.5)
+
+    ms_kernel = time_kernel(one, iters=4 * n_layers)
+    reset_context()
+    return dict(ms_per_step=ms_step, flops_per_call=flops_call, bytes_per_call=bytes_call,
+                tflops_step=flops_call * n_layers / (ms_step * 1e-3) / 1e12,
+                kernel_us=ms_kernel * 1e3, tflops_kernel=flops_call / (ms_kernel * 1e-3) / 1e12)
+
+
+def bench_block_cached(dev, quick):
+    """C5: 32 x 32-token blocks against 2-4k-token cached prefixes in shuffled
+    256-row pages (LLaDA shape); the prefix is written with store_kvcache."""
+    from oracle import configs
+    from dllm_serve_amd import _capi
+    from dllm_serve_amd.layers.attention import store_kvcache
+
+    c = configs.c5_cached()
+    Hq = Hkv = 32
+    D = 128
+    page = c["page"]
+    kc = torch.zeros(c["num_pages"] * page, Hkv, D, dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    slots = torch.tensor([x for s in c["slots"] for x in s], dtype=torch.int32, device=dev)
+    k_pre, v_pre = c["k_pre"].to(dev), c["v_pre"].to(dev)
+    n_pre = k_pre.shape[0]
+    ms_store = time_kernel(lambda: store_kvcache(k_pre, v_pre, kc.view(-1, page, Hkv, D),
+                                                 vc.view(-1, page, Hkv, D), slots), iters=20)
+    store_bytes = 8.0 * n_pre * Hkv * D + 4.0 * n_pre
+    q, k, v = c["q"].to(dev), c["k"].to(dev), c["v"].to(dev)
+    B, blk = len(c["prefix"]), c["blk"]
+    cu = torch.arange(0, (B + 1) * blk, blk, dtype=torch.int32, device=dev)
+    off = [0]
+    for p in c["prefix"]:
+        off.append(off[-1] + p)
+    slot_off = torch.tensor(off, dtype=torch.int32, device=dev)
+    max_keys = max(c["prefix"]) + blk
+    ws_b = _capi.block_cached_workspace_size(B, blk, max_keys, Hq, Hkv, D)
+    ws = torch.empty(max(ws_b, 1), dtype=torch.uint8, device=dev)
+    o = torch.empty_like(q)
+    ms = time_kernel(lambda: _capi.attn_block_cached_fwd(q, k, v, o, cu, None, B, blk, max_keys, kc, vc, slots,
+                                                         slot_off, D ** -0.5, ws if ws_b else None), iters=50)
+    flops = sum(4.0 * blk * (p + blk) * Hq * D for p in c["prefix"])
+    byts = sum(2.0 * (2 * blk * Hq * D + 2 * (p + blk) * Hkv * D) + 4.0 * p for p in c["prefix"])
+    return dict(kernel_us=ms * 1e3, gbs=byts / (ms * 1e-3) / 1e9, tflops=flops / (ms * 1e-3) / 1e12,
+                bytes_per_call=byts, store_us=ms_store * 1e3, store_gbs=store_bytes / (ms_store * 1e-3) / 1e9)
+
+
+def bench_sparse_c4(dev, steps_block=64, quick=False):
+    """C4 attention per 64-step block (B=4, P=1024, gen 256, block 64, LLaDA
+    shape): sparse = head_select retention 0.5 (1 full step, 1 full step +
+    selection/store, 62 reuse steps); dense = 64 full recompute steps."""
+    from dllm_serve_amd.engine.sequence import PageAllocator, Sequence, prepare_step
+    from dllm_serve_amd.layers.attention import Attention
+    from dllm_serve_amd.sparse.state import SparseConfig
+    from dllm_serve_amd.utils.context import reset_context
+
+    Hq = Hkv = 32
+    D = 128
+    B, P, gen, blk = 4, 1024, 256, 64
+
+    def run(cfg):
+        attn = Attention(Hq, D, D ** -0.5, Hkv, causal=False)
+        pages = 4 * 8
+        cache = torch.zeros(2, pages, 256, Hkv, D, dtype=torch.bfloat16, device=dev)
+        attn.k_cache, attn.v_cache = cache[0], cache[1]
+        seqs = [Sequence([1] * P, gen, 126336, cfg, device=dev, steps=gen) for _ in range(B)]
+        alloc = PageAllocator(range(pages))
+        if cfg is not None:
+            for s in seqs:
+                alloc.allocate(s)
+        g = torch.Generator(device=dev).manual_seed(1)
+        full = (torch.randn(B * (P + gen), Hq, D, generator=g, device=dev, dtype=torch.bfloat16),
+                torch.randn(B * (P + gen), Hkv, D, generator=g, device=dev, dtype=torch.bfloat16),
+                torch.randn(B * (P + gen), Hkv, D, generator=g, device=dev, dtype=torch.bfloat16))
+        blkq = tuple(t[:B * blk] for t in full)
+        torch.cuda.synchronize()
+        total = 0.0
+        for step in range(steps_block):
+            prepare_step(seqs, dev)
+            rows = sum(s.step_rows()[1] for s in seqs)
+            q, k, v = (blkq if rows == B * blk else full)
+            from dllm_serve_amd.utils.context import get_context
+            attn._plan(get_context(), dev)  # per-step host plan, shared by all layers: not timed
+            t = Timer()
+            t.start()
+            attn(q[:rows], k[:rows], v[:rows])
+            total += t.stop_ms()
+            reset_context()
+            for s in seqs:
+                s.advance()
+        return total
+
+    ms_sparse = run(SparseConfig(enabled=True, default_block_len=blk, retention_ratio=0.5, pool_kernel=3,
+                                 delay_step=1, head_select=True))
+    ms_cached_full = run(SparseConfig(enabled=True, default_block_len=blk, retention_ratio=1.0, pool_kernel=3,
+                                      delay_step=1, head_select=True))
+    ms_dense = run(None)
+    return dict(ms_per_block_sparse=ms_sparse, ms_per_block_ret1=ms_cached_full, ms_per_block_dense=ms_dense,
+                speedup_vs_dense=ms_dense / ms_sparse, speedup_vs_ret1=ms_cached_full / ms_sparse)
+
+
+def cpu_baseline(lens, Hq, Hkv, D, budget_s=12.0):
+    """Oracle (numpy fp32) attention of the headline step's layer calls on the
+    host cores; bounded sample of whole layer calls."""
+    from oracle import attention as oatt
+    from oracle.configs import attention_flops, packed_qkv
+
+    q, k, v, cu = packed_qkv(lens, Hq, Hkv, D, seed=0, dtype=torch.float32)
+    qn, kn, vn, cun = q.numpy(), k.numpy(), v.numpy(), cu.numpy()
+    oatt.varlen(qn[:cun[1]], kn[:cun[1]], vn[:cun[1]], cun[:2], cun[:2], D ** -0.5, dtype=np.float32)  # warm
+    t0 = time.perf_counter()
+    calls = 0
+    while True:
+        oatt.varlen(qn, kn, vn, cun, cun, D ** -0.5, dtype=np.float32)
+        calls += 1
+        if time.perf_counter() - t0 > budget_s or calls >= 64:
+            break
+    dt = time.perf_counter() - t0
+    flops = attention_flops(lens, lens, Hq, D) * calls
+    cores = len(os.sched_getaffinity(0))
+    return dict(value=flops / dt / 1e12, unit="TFLOP/s", cores=cores, kind="port",
+                sample=f"{calls} layer call(s) of the headline step (8 x 384 tokens, 32 heads x 128), "
+                       f"numpy fp32 oracle, {dt:.1f} s, threads = BLAS default on {cores} host cores")
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--quick", action="store_true", help="headline only (no extra shapes, no CPU baseline)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); this build has no multi-GPU path",
+              file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    from dllm_serve_amd import _capi
+
+    _capi.load()
+    dev = torch.device("cuda:0")
+    Hq = Hkv = 32
+    D = 128
+    lens = [256 + 128] * 8
+    n_layers = 32
+    log("headline: C2 dense step attention, 32 layers x 8 x 384 tokens")
+    r = bench_dense(lens, Hq, Hkv, D, n_layers, args.steps, args.warmup, dev)
+    extra = {}
+    if not args.quick:
+        log("C3: Dream-7B GQA 28/4 varlen")
+        from oracle.configs import c3_lens
+        c3 = c3_lens()
+        r3 = bench_dense(c3, 28, 4, D, 4, 3, 1, dev, seed=3)
+        extra["c3_dream_gqa_varlen"] = dict(lens=c3, kernel_us=round(r3["kernel_us"], 2),
+                                            tflops=round(r3["tflops_kernel"], 1))
+        log("C4 full-step shape: 4 x 1280 tokens")
+        r4 = bench_dense([1280] * 4, Hq, Hkv, D, 4, 3, 1, dev, seed=4)
+        extra["c4_full_step_attention"] = dict(kernel_us=round(r4["kernel_us"], 2),
+                                               tflops=round(r4["tflops_kernel"], 1),
+                                               frac_of_peak=round(r4["tflops_kernel"] / PEAK_BF16_TFLOPS, 4))
+        log("C5: block-cached attention + KV scatter")
+        r5 = bench_block_cached(dev, args.quick)
+        extra["c5_block_cached"] = {k: round(v, 3) for k, v in r5.items()}
+        log("C4: sparse vs dense attention per 64-step block")
+        r4s = bench_sparse_c4(dev)
+        extra["c4_head_sparse_per_block"] = {k: round(v, 3) for k, v in r4s.items()}
+    cpu = None
+    if not args.quick:
+        log("CPU baseline (oracle)")
+        cpu = cpu_baseline(lens, Hq, Hkv, D)
+        cpu["value"] = round(cpu["value"], 4)
+    achieved = r["tflops_kernel"]
+    line = {
+        "metric": METRIC,
+        "value": round(r["tflops_step"], 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(r["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "LLaDA-8B dense denoise-step attention: 32 layers x 8 sequences x 384 tokens "
+                               "(prompt 256 + gen 128), 32 heads x 128, non-causal varlen",
+                   "global_batch": 8, "seq_len": 384, "layers": n_layers},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "kernel": "attn_fwd_kernel<4,1,2,false>", "kernel_us": round(r["kernel_us"], 3),
+                     "flops_per_launch": r["flops_per_call"], "algorithmic_bytes_per_launch": r["bytes_per_call"]},
+        "cpu_baseline": cpu,
+    }
+    line.update(extra)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

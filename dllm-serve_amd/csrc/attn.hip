@@ -27,6 +27,8 @@
 
 #include <math.h>
 
+#include <type_traits>
+
 namespace dllm {
 
 constexpr int HD = 128;       // head dim handled by this build
@@ -82,55 +84,34 @@ __device__ __forceinline__ int xcd_remap(int b, int nb) {
   return (b & 7) * per + (b >> 3);
 }
 
-// Address of key/value row `kidx` of a segment for KV head hkv (nullptr: zero row).
-template <bool CACHED>
-__device__ __forceinline__ const uint16_t* kv_row(const uint16_t* base, const uint16_t* cache, int64_t stride,
-                                                  const AttnArgs& a, const SegDesc& sd, int hkv, int kidx) {
-  if (CACHED && kidx < sd.n_c) {
-    const int64_t s = a.slots[sd.slot_base + kidx];
-    if (s < 0 || s >= a.cache_slots) return nullptr;
-    return cache + s * (int64_t)(a.Hkv * HD) + hkv * HD;
-  }
-  return base + (int64_t)(sd.krow0 + kidx - (CACHED ? sd.n_c : 0)) * stride + hkv * HD;
+__device__ __forceinline__ u32x4_t zero_unless(u32x4_t v, bool ok) {
+  u32x4_t r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r[i] = ok ? v[i] : 0u;
+  return r;
 }
 
-template <int WM, int WK, int KBW, bool CACHED>
-struct TileIO {
+// Buffer resource over [base, base + bytes): loads at offsets >= bytes return
+// zero, which is how rows past the end of a segment read as zero without any
+// per-lane clamping.  The whole offset is passed in the VGPR operand (the
+// scalar offset is kept 0 so the range check covers it); offsets are 32-bit
+// byte offsets from base, which the host checks cannot overflow.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ u32x4_t bload(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0));
+}
+
+// Where each thread's 16-byte pieces of a key tile go:
+//   K: rows (tid >> 4) + 16 i, chunk tid & 15               (i < KCH)
+//   V: 4 rows 4 kg + e of the 8-element column chunk dc      (i < VGR)
+//      with idx = tid + 256 i, kg = idx % (NKT/4), dc = idx / (NKT/4)
+template <int WM, int WK, int KBW>
+struct TileRegs {
   using C = Cfg<WM, WK, KBW>;
   u32x4_t kr[C::KCH];
   u32x4_t vr[C::VGR][4];
-
-  __device__ __forceinline__ void load(const AttnArgs& a, const SegDesc& sd, int hkv, int k0, int kend) {
-    const int tid = threadIdx.x;
-#pragma unroll
-    for (int i = 0; i < C::KCH; ++i) {
-      const int row = (tid >> 4) + 16 * i;
-      const int ch = tid & 15;
-      const int kidx = k0 + row;
-      u32x4_t val = {0u, 0u, 0u, 0u};
-      if (kidx < kend) {
-        const uint16_t* p = kv_row<CACHED>(a.k, a.k_cache, a.k_stride, a, sd, hkv, kidx);
-        if (p) val = ld128(p + ch * 8);
-      }
-      kr[i] = val;
-    }
-#pragma unroll
-    for (int i = 0; i < C::VGR; ++i) {
-      const int idx = tid + 256 * i;
-      const int kg = idx % (C::NKT / 4);
-      const int dc = idx / (C::NKT / 4);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int kidx = k0 + kg * 4 + e;
-        u32x4_t val = {0u, 0u, 0u, 0u};
-        if (kidx < kend) {
-          const uint16_t* p = kv_row<CACHED>(a.v, a.v_cache, a.v_stride, a, sd, hkv, kidx);
-          if (p) val = ld128(p + dc * 8);
-        }
-        vr[i][e] = val;
-      }
-    }
-  }
 
   __device__ __forceinline__ void store(uint16_t* buf) const {
     const int tid = threadIdx.x;
@@ -155,10 +136,10 @@ struct TileIO {
       for (int w = 0; w < 4; ++w) {  // word w holds d = dc*8 + 2w (low half), 2w+1 (high half)
         const uint32_t a0 = vr[i][0][w], a1 = vr[i][1][w], a2 = vr[i][2][w], a3 = vr[i][3][w];
         u32x2_t lo, hi;
-        lo[0] = (a0 & 0xffffu) | (a1 << 16);
-        lo[1] = (a2 & 0xffffu) | (a3 << 16);
-        hi[0] = (a0 >> 16) | (a1 & 0xffff0000u);
-        hi[1] = (a2 >> 16) | (a3 & 0xffff0000u);
+        lo[0] = __builtin_amdgcn_perm(a1, a0, 0x05040100u);
+        lo[1] = __builtin_amdgcn_perm(a3, a2, 0x05040100u);
+        hi[0] = __builtin_amdgcn_perm(a1, a0, 0x07060302u);
+        hi[1] = __builtin_amdgcn_perm(a3, a2, 0x07060302u);
         const int d = dc * 8 + 2 * w;
         *reinterpret_cast<u32x2_t*>(Vt + d * C::VSTR + pos) = lo;
         *reinterpret_cast<u32x2_t*>(Vt + (d + 1) * C::VSTR + pos) = hi;
@@ -166,6 +147,210 @@ struct TileIO {
     }
   }
 };
+
+// Dense segments: K/V rows are contiguous token rows of the segment.  All
+// address arithmetic is scalar except one 32-bit base offset per piece.
+template <int WM, int WK, int KBW>
+struct DenseLoader : TileRegs<WM, WK, KBW> {
+  using C = Cfg<WM, WK, KBW>;
+  __amdgpu_buffer_rsrc_t krs, vrs;
+  uint32_t kS, vS;               // token stride in bytes
+  uint32_t k_off;                // this thread's K piece offset for tile row 0
+  uint32_t v_off[C::VGR];        // this thread's V piece offsets for tile row 0
+
+  __device__ __forceinline__ void init(const AttnArgs& a, const SegDesc& sd, int hkv) {
+    const int tid = threadIdx.x;
+    kS = (uint32_t)(a.k_stride * 2);
+    vS = (uint32_t)(a.v_stride * 2);
+    const uint16_t* kb = a.k + (int64_t)sd.krow0 * a.k_stride + hkv * HD;
+    const uint16_t* vb = a.v + (int64_t)sd.krow0 * a.v_stride + hkv * HD;
+    const int Lk = sd.Lkb;
+    krs = make_rsrc(kb, Lk > 0 ? (uint32_t)(Lk - 1) * kS + HD * 2 : 0u);
+    vrs = make_rsrc(vb, Lk > 0 ? (uint32_t)(Lk - 1) * vS + HD * 2 : 0u);
+    k_off = (uint32_t)(tid >> 4) * kS + (uint32_t)(tid & 15) * 16u;
+#pragma unroll
+    for (int i = 0; i < C::VGR; ++i) {
+      const int idx = tid + 256 * i;
+      const int kg = idx % (C::NKT / 4);
+      const int dc = idx / (C::NKT / 4);
+      v_off[i] = (uint32_t)(kg * 4) * vS + (uint32_t)dc * 16u;
+    }
+  }
+
+  __device__ __forceinline__ void load(int k0) {
+#pragma unroll
+    for (int i = 0; i < C::KCH; ++i) this->kr[i] = bload(krs, k_off + (uint32_t)(k0 + 16 * i) * kS, 0u);
+#pragma unroll
+    for (int i = 0; i < C::VGR; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) this->vr[i][e] = bload(vrs, v_off[i] + (uint32_t)(k0 + e) * vS, 0u);
+  }
+};
+
+// Cached segments (mode 2): key index kidx < n_c reads cache row
+// slots[slot_base + kidx]; n_c <= kidx < n_c + Lkb reads block row kidx - n_c.
+// The slots of the next-but-one tile are fetched while the next tile's rows
+// are loaded, so no tile waits on its own slot indirection.
+template <int WM, int WK, int KBW>
+struct CachedLoader : TileRegs<WM, WK, KBW> {
+  using C = Cfg<WM, WK, KBW>;
+  const AttnArgs* ap;
+  const int32_t* sp;   // this segment's slots (a valid dummy when it has none)
+  int hkv, kend, n_c, krow0, Lkb;
+  int sk[C::KCH];      // slots of this thread's K rows of the pending tile
+  int sv[C::VGR][4];   // slots of this thread's V rows of the pending tile
+
+  __device__ __forceinline__ void init(const AttnArgs& a, const SegDesc& sd, int hkv_, int kend_) {
+    ap = &a;
+    hkv = hkv_;
+    kend = kend_;
+    n_c = sd.n_c;
+    krow0 = sd.krow0;
+    Lkb = sd.Lkb;
+    sp = n_c > 0 ? a.slots + sd.slot_base : a.slot_off;
+  }
+
+  // Slot of cached row kidx; the index is clamped into the segment's slot
+  // list so the (unconditional) load is always in bounds.
+  __device__ __forceinline__ int slot_at(int kidx) const { return sp[min(max(kidx, 0), max(n_c - 1, 0))]; }
+
+  __device__ __forceinline__ void fetch_slots(int k0) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < C::KCH; ++i) sk[i] = slot_at(k0 + (tid >> 4) + 16 * i);
+#pragma unroll
+    for (int i = 0; i < C::VGR; ++i) {
+      const int kg = (tid + 256 * i) % (C::NKT / 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sv[i][e] = slot_at(k0 + kg * 4 + e);
+    }
+  }
+
+  __device__ __forceinline__ u32x4_t row_piece(const uint16_t* cache, const uint16_t* blk, int64_t stride, int slot,
+                                               int kidx, int col) const {
+    const AttnArgs& a = *ap;
+    const bool in_range = kidx < kend;
+    const bool cached = kidx < n_c;
+    const bool slot_ok = slot >= 0 && (int64_t)slot < a.cache_slots;
+    const uint16_t* p;
+    if (cached)
+      p = cache + (int64_t)(slot_ok ? slot : 0) * (a.Hkv * HD) + hkv * HD;
+    else
+      p = blk + (int64_t)(krow0 + min(max(kidx - n_c, 0), Lkb - 1)) * stride + hkv * HD;
+    return zero_unless(ld128(p + col), in_range && (!cached || slot_ok));
+  }
+
+  __device__ __forceinline__ void load(int k0) {
+    const AttnArgs& a = *ap;
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < C::KCH; ++i)
+      this->kr[i] = row_piece(a.k_cache, a.k, a.k_stride, sk[i], k0 + (tid >> 4) + 16 * i, (tid & 15) * 8);
+#pragma unroll
+    for (int i = 0; i < C::VGR; ++i) {
+      const int idx = tid + 256 * i;
+      const int kg = idx % (C::NKT / 4);
+      const int dc = idx / (C::NKT / 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        this->vr[i][e] = row_piece(a.v_cache, a.v, a.v_stride, sv[i][e], k0 + kg * 4 + e, dc * 8);
+    }
+  }
+};
+
+// Running softmax state of one wavefront (M row = lane % 32).  The reference
+// maximum m_run (log2 domain) is only raised when a new score exceeds it by
+// more than kLazy, so most tiles skip rescaling O; probabilities then stay
+// below 2^kLazy, well inside the bf16 / fp32 range.
+constexpr float kLazy = 8.0f;
+
+template <int KBW>
+struct WaveState {
+  f32x16_t oacc[4];
+  float m_run;  // reference maximum, log2 domain
+  float l_run;  // this lane's half of the row sum
+};
+
+// One key tile for one wavefront: S^T = K Q^T, online softmax, O^T += V^T P^T.
+template <int WM, int WK, int KBW, bool MASK>
+__device__ __forceinline__ void tile_compute(const uint16_t* Ks, const uint16_t* Vt, const bf16x8_t (&qf)[8],
+                                             WaveState<KBW>& st, float c, int k_valid) {
+  using C = Cfg<WM, WK, KBW>;
+  const int lane = threadIdx.x & 63;
+  const int lrow = lane & 31;
+  const int hl = lane >> 5;
+  const int wk = (threadIdx.x >> 6) / WM;
+
+  f32x16_t sacc[KBW];
+#pragma unroll
+  for (int b = 0; b < KBW; ++b) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) sacc[b][i] = 0.f;
+    const int kb = wk * KBW + b;
+    const uint16_t* kp = Ks + (kb * 32 + lrow) * KSTR + hl * 8;
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
+      const bf16x8_t af = as_bf16x8(*reinterpret_cast<const u32x4_t*>(kp + kk * 16));
+      sacc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, qf[kk], sacc[b], 0, 0, 0);
+    }
+  }
+
+  float mx = -INFINITY;
+#pragma unroll
+  for (int b = 0; b < KBW; ++b) {
+    const int kb = wk * KBW + b;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      if (MASK) {
+        const int key = kb * 32 + 8 * (i >> 2) + 4 * hl + (i & 3);
+        if (key >= k_valid) sacc[b][i] = -INFINITY;
+      }
+      mx = fmaxf(mx, sacc[b][i]);
+    }
+  }
+  mx = fmaxf(mx, __shfl_xor(mx, 32)) * c;  // c > 0: scaling commutes with max
+  const bool need = mx > st.m_run + kLazy;
+  if (__builtin_amdgcn_ballot_w64(need)) {
+    const float m_new = need ? mx : st.m_run;
+    const float alpha = (st.m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(st.m_run - m_new);
+    st.l_run *= alpha;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) st.oacc[db][i] *= alpha;
+    st.m_run = m_new;
+  }
+  const float neg_m = (st.m_run == -INFINITY) ? 0.f : -st.m_run;
+
+  float psum = 0.f;
+  bf16x8_t pf[2 * KBW];
+#pragma unroll
+  for (int b = 0; b < KBW; ++b) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      u32x4_t pk;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[b][8 * j + 2 * w], c, neg_m));
+        const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[b][8 * j + 2 * w + 1], c, neg_m));
+        psum += p0 + p1;
+        pk[w] = cvt_pk_bf16(p0, p1);
+      }
+      pf[2 * b + j] = as_bf16x8(pk);
+    }
+  }
+  st.l_run += psum;
+
+#pragma unroll
+  for (int db = 0; db < 4; ++db) {
+    const uint16_t* vp = Vt + (db * 32 + lrow) * C::VSTR + wk * KBW * 32 + hl * 8;
+#pragma unroll
+    for (int cch = 0; cch < 2 * KBW; ++cch) {
+      const bf16x8_t af = as_bf16x8(*reinterpret_cast<const u32x4_t*>(vp + cch * 16));
+      st.oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, pf[cch], st.oacc[db], 0, 0, 0);
+    }
+  }
+}
 
 template <int WM, int WK, int KBW, bool CACHED>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WK == 1 ? 2 : 1, WK == 1 ? 2 : 1))) void attn_fwd_kernel(AttnArgs a) {
@@ -222,121 +407,73 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WK == 1 ? 2
   const int wk = wave / WM;
 
   // ---- Q^T fragments (B operand of S^T = K Q^T), resident for the whole loop.
+  // Rows past the segment (M tail) read as zero through the buffer bound.
   const int m = m_base + wm * 32 + lrow;
   const bool m_ok = m < M;
   const int tok = m_ok ? m / g : 0;
   const int head = hkv * g + (m_ok ? m - tok * g : 0);
   bf16x8_t qf[8];
   {
-    const uint16_t* qp = a.q + (int64_t)(sd.qrow0 + tok) * a.q_stride + head * HD + hl * 8;
+    const uint32_t qS = (uint32_t)(a.q_stride * 2);
+    const __amdgpu_buffer_rsrc_t qrs =
+        make_rsrc(a.q + (int64_t)sd.qrow0 * a.q_stride, sd.Lq > 0 ? (uint32_t)sd.Lq * qS : 0u);
+
+    const uint32_t qbytes = sd.Lq > 0 ? (uint32_t)sd.Lq * qS : 0u;
+    const uint32_t qoff = m_ok ? (uint32_t)tok * qS + (uint32_t)(head * HD + hl * 8) * 2u : qbytes;
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk) {
-      u32x4_t t = {0u, 0u, 0u, 0u};
-      if (m_ok) t = ld128(qp + kk * 16);
-      qf[kk] = as_bf16x8(t);
-    }
+    for (int kk = 0; kk < 8; ++kk) qf[kk] = as_bf16x8(bload(qrs, qoff + (uint32_t)kk * 32u, 0u));
   }
 
-  f32x16_t oacc[4];
+  WaveState<KBW> st;
 #pragma unroll
   for (int db = 0; db < 4; ++db)
 #pragma unroll
-    for (int i = 0; i < 16; ++i) oacc[db][i] = 0.f;
-  float m_run = -INFINITY;
-  float l_run = 0.f;  // this lane's half of the row sum
+    for (int i = 0; i < 16; ++i) st.oacc[db][i] = 0.f;
+  st.m_run = -INFINITY;
+  st.l_run = 0.f;
+  const float c = a.scale_log2;
 
   const int ntiles = (kend - kbeg + C::NKT - 1) / C::NKT;
-  TileIO<WM, WK, KBW, CACHED> io;
+  using Loader = typename std::conditional<CACHED, CachedLoader<WM, WK, KBW>, DenseLoader<WM, WK, KBW>>::type;
+  Loader io;
+  if constexpr (CACHED) {
+    io.init(a, sd, hkv, kend);
+    io.fetch_slots(kbeg);
+  } else {
+    io.init(a, sd, hkv);
+  }
   if (ntiles > 0) {
-    io.load(a, sd, hkv, kbeg, kend);
+    io.load(kbeg);
+    if constexpr (CACHED) io.fetch_slots(kbeg + C::NKT);
     io.store(smem);
   }
   __syncthreads();
 
-  for (int t = 0; t < ntiles; ++t) {
+  // Full tiles with the next tile's loads in flight; the last (possibly
+  // partial) tile is peeled off and masked.
+  for (int t = 0; t + 1 < ntiles; ++t) {
     const int k0 = kbeg + t * C::NKT;
-    const bool more = t + 1 < ntiles;
-    if (more) io.load(a, sd, hkv, k0 + C::NKT, kend);
-
+    io.load(k0 + C::NKT);
+    if constexpr (CACHED) io.fetch_slots(k0 + 2 * C::NKT);
     const uint16_t* Ks = smem + (t & 1) * C::BUF_ELEMS;
-    const uint16_t* Vt = Ks + C::K_ELEMS;
-
-    // ---- S^T for this wavefront's key blocks
-    f32x16_t sacc[KBW];
-#pragma unroll
-    for (int b = 0; b < KBW; ++b) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) sacc[b][i] = 0.f;
-      const int kb = wk * KBW + b;
-      const uint16_t* kp = Ks + (kb * 32 + lrow) * KSTR + hl * 8;
-#pragma unroll
-      for (int kk = 0; kk < 8; ++kk) {
-        const bf16x8_t af = as_bf16x8(*reinterpret_cast<const u32x4_t*>(kp + kk * 16));
-        sacc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, qf[kk], sacc[b], 0, 0, 0);
-      }
-    }
-
-    // ---- online softmax (log2 domain)
-    const bool tail = k0 + C::NKT > kend;
-    float mx = -INFINITY;
-#pragma unroll
-    for (int b = 0; b < KBW; ++b) {
-      const int kb = wk * KBW + b;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        float x = sacc[b][i] * a.scale_log2;
-        if (tail) {
-          const int key = k0 + kb * 32 + 8 * (i >> 2) + 4 * hl + (i & 3);
-          if (key >= kend) x = -INFINITY;
-        }
-        sacc[b][i] = x;
-        mx = fmaxf(mx, x);
-      }
-    }
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m_run, mx);
-    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-    float psum = 0.f;
-    bf16x8_t pf[2 * KBW];
-#pragma unroll
-    for (int b = 0; b < KBW; ++b) {
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        u32x4_t pk;
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          const float p0 = __builtin_amdgcn_exp2f(sacc[b][8 * j + 2 * w] - m_use);
-          const float p1 = __builtin_amdgcn_exp2f(sacc[b][8 * j + 2 * w + 1] - m_use);
-          psum += p0 + p1;
-          pk[w] = pack_bf16x2(p0, p1);
-        }
-        pf[2 * b + j] = as_bf16x8(pk);
-      }
-    }
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
-#pragma unroll
-    for (int db = 0; db < 4; ++db)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) oacc[db][i] *= alpha;
-
-    // ---- O^T += V^T P^T
-#pragma unroll
-    for (int db = 0; db < 4; ++db) {
-      const uint16_t* vp = Vt + (db * 32 + lrow) * C::VSTR + wk * KBW * 32 + hl * 8;
-#pragma unroll
-      for (int c = 0; c < 2 * KBW; ++c) {
-        const bf16x8_t af = as_bf16x8(*reinterpret_cast<const u32x4_t*>(vp + c * 16));
-        oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, pf[c], oacc[db], 0, 0, 0);
-      }
-    }
-
-    if (more) io.store(smem + ((t + 1) & 1) * C::BUF_ELEMS);
+    tile_compute<WM, WK, KBW, false>(Ks, Ks + C::K_ELEMS, qf, st, c, C::NKT);
+    io.store(smem + ((t + 1) & 1) * C::BUF_ELEMS);
     __syncthreads();
   }
+  if (ntiles > 0) {
+    const int t = ntiles - 1;
+    const int k_valid = kend - (kbeg + t * C::NKT);
+    const uint16_t* Ks = smem + (t & 1) * C::BUF_ELEMS;
+    if (k_valid < C::NKT)
+      tile_compute<WM, WK, KBW, true>(Ks, Ks + C::K_ELEMS, qf, st, c, k_valid);
+    else
+      tile_compute<WM, WK, KBW, false>(Ks, Ks + C::K_ELEMS, qf, st, c, C::NKT);
+  }
+  __syncthreads();
 
-  const float l_tot = l_run + __shfl_xor(l_run, 32);
+  const float m_run = st.m_run;
+  const float l_tot = st.l_run + __shfl_xor(st.l_run, 32);
+  f32x16_t (&oacc)[4] = st.oacc;
 
   if constexpr (WK == 1) {
     // ---- direct epilogue: normalise and store bf16
@@ -369,7 +506,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WK == 1 ? 2
 #pragma unroll
     for (int w = 0; w < WK; ++w) m_all = fmaxf(m_all, red_m[w * 32 + lrow]);
     const float m_all_use = (m_all == -INFINITY) ? 0.f : m_all;
-    const float fac = __builtin_amdgcn_exp2f(m_run - m_all_use);
+    const float fac = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run - m_all_use);
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
@@ -387,7 +524,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WK == 1 ? 2
     const float mq_use = (mq == -INFINITY) ? 0.f : mq;
     float lq = 0.f;
 #pragma unroll
-    for (int w = 0; w < WK; ++w) lq += red_l[w * 32 + q] * __builtin_amdgcn_exp2f(red_m[w * 32 + q] - mq_use);
+    for (int w = 0; w < WK; ++w) {
+      const float mw = red_m[w * 32 + q];
+      lq += (mw == -INFINITY) ? 0.f : red_l[w * 32 + q] * __builtin_amdgcn_exp2f(mw - mq_use);
+    }
     float acc[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
@@ -459,7 +599,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
   float l = 0.f, acc = 0.f;
   for (int sp = 0; sp < a.n_split; ++sp) {
     const float* rec = ml + ((P0 + sp) * 32 + q) * 2;
-    const float w = __builtin_amdgcn_exp2f(rec[0] - mu);
+    const float w = (rec[0] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(rec[0] - mu);
     l += rec[1] * w;
     acc += a.ws[((P0 + sp) * 32 + q) * HD + d] * w;
   }
@@ -504,7 +644,7 @@ using namespace dllm;
 
 extern "C" int dllm_attn_varlen_fwd(const dllm_bf16* q, const dllm_bf16* k, const dllm_bf16* v, dllm_bf16* o,
                                     const int32_t* cu_q, const int32_t* cu_k, const int32_t* seg_ids, int n_seg,
-                                    int max_seqlen_q, int Hq, int Hkv, int D, int64_t q_stride_tok,
+                                    int max_seqlen_q, int max_seqlen_k, int Hq, int Hkv, int D, int64_t q_stride_tok,
                                     int64_t k_stride_tok, int64_t v_stride_tok, int64_t o_stride_tok,
                                     float softmax_scale, void* stream) {
   const char* name = "dllm_attn_varlen_fwd";
@@ -513,6 +653,14 @@ extern "C" int dllm_attn_varlen_fwd(const dllm_bf16* q, const dllm_bf16* k, cons
   if (n_seg < 0 || max_seqlen_q < 0) return fail(DLLM_ERR_INVALID_ARG, "%s: negative n_seg / max_seqlen_q", name);
   if (n_seg == 0 || max_seqlen_q == 0) return DLLM_OK;
   if (!cu_q || !cu_k) return fail(DLLM_ERR_INVALID_ARG, "%s: null cu_seqlens", name);
+  if (max_seqlen_k < 0) return fail(DLLM_ERR_INVALID_ARG, "%s: negative max_seqlen_k", name);
+  {
+    // per-segment byte offsets are 32-bit (buffer loads)
+    const int64_t kvs = k_stride_tok > v_stride_tok ? k_stride_tok : v_stride_tok;
+    if ((int64_t)max_seqlen_k * kvs * 2 + 4096 >= ((int64_t)1 << 32) ||
+        (int64_t)max_seqlen_q * q_stride_tok * 2 + 4096 >= ((int64_t)1 << 32))
+      return fail(DLLM_ERR_UNSUPPORTED, "%s: a segment spans more than 4 GiB of q/k/v", name);
+  }
   AttnArgs a = {};
   a.q = q; a.k = k; a.v = v; a.o = o;
   a.cu_q = cu_q; a.cu_k = cu_k; a.seg_ids = seg_ids;
@@ -573,6 +721,8 @@ extern "C" int dllm_attn_block_cached_fwd(const dllm_bf16* q, const dllm_bf16* k
   if (n_seg < 0 || max_q < 0 || max_keys < 0) return fail(DLLM_ERR_INVALID_ARG, "%s: negative size", name);
   if (n_seg == 0 || max_q == 0) return DLLM_OK;
   if (!cu || !slot_off) return fail(DLLM_ERR_INVALID_ARG, "%s: null cu / slot_off", name);
+  if ((int64_t)max_q * q_stride_tok * 2 + 4096 >= ((int64_t)1 << 32))
+    return fail(DLLM_ERR_UNSUPPORTED, "%s: a block spans more than 4 GiB of q", name);
   if (cache_slots > 0 && (!k_cache || !v_cache || !slots))
     return fail(DLLM_ERR_INVALID_ARG, "%s: null cache / slots", name);
   if (cache_slots > 0 && (!aligned16(k_cache) || !aligned16(v_cache)))

@@ -37,7 +37,7 @@ SIGNATURES = {
     "dllm_load_kvcache": (_I, [_P, _I64, _P, _I64, _P, _P, _I64, _P, _I, _I, _P]),
     "dllm_attn_varlen_fwd": (
         _I,
-        [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I64, _I64, _I64, _I64, _F, _P],
+        [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I64, _I64, _I64, _I64, _F, _P],
     ),
     "dllm_attn_block_cached_workspace_size": (_SZ, [_I, _I, _I, _I, _I, _I]),
     "dllm_attn_block_cached_fwd": (
@@ -125,13 +125,15 @@ def load_kvcache(key, value, k_cache, v_cache, slot_mapping, n_tok, row_elems):
     _check(rc, "dllm_load_kvcache")
 
 
-def attn_varlen_fwd(q, k, v, o, cu_q, cu_k, seg_ids, n_seg, max_seqlen_q, scale):
+def attn_varlen_fwd(q, k, v, o, cu_q, cu_k, seg_ids, n_seg, max_seqlen_q, scale, max_seqlen_k=None):
     """K3a: bidirectional varlen attention of segments (q,k,v,o are [rows, H, D])."""
     _require_gpu(q, k, v, o, cu_q, cu_k)
     lib = load()
+    if max_seqlen_k is None:
+        max_seqlen_k = max_seqlen_q
     rc = lib.dllm_attn_varlen_fwd(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
-        cu_q.data_ptr(), cu_k.data_ptr(), _ptr(seg_ids), n_seg, max_seqlen_q,
+        cu_q.data_ptr(), cu_k.data_ptr(), _ptr(seg_ids), n_seg, max_seqlen_q, max_seqlen_k,
         q.shape[1], k.shape[1], q.shape[2],
         q.stride(0), k.stride(0), v.stride(0), o.stride(0), float(scale),
         _stream(q.device))

@@ -83,15 +83,16 @@ int dllm_load_kvcache(dllm_bf16* key, int64_t key_stride_tok,
  * seg_ids lets a caller run a subset of the sequences of one packed batch in
  * place, without packing copies.  For every q row t of segment s and head h:
  *   o[t, h] = sum_u softmax_u(scale * q[t, h] . k[u, h / (Hq/Hkv)]) v[u, h / (Hq/Hkv)]
- * bf16 inputs, fp32 accumulation, bf16 output.  max_seqlen_q must bound every
- * segment's q length (it sizes the grid, as in flash-attn).  D must be 128;
+ * bf16 inputs, fp32 accumulation, bf16 output.  max_seqlen_q / max_seqlen_k
+ * must bound every segment's q / k length (as in flash-attn; max_seqlen_q
+ * sizes the grid).  A segment may span at most 4 GiB of q, k or v.  D must be 128;
  * Hq must be a multiple of Hkv.  Pointers must be 16-byte aligned and the
  * token strides multiples of 8 elements.  Rows of o outside the segments are
  * not written.
  */
 int dllm_attn_varlen_fwd(const dllm_bf16* q, const dllm_bf16* k, const dllm_bf16* v, dllm_bf16* o,
                          const int32_t* cu_q, const int32_t* cu_k, const int32_t* seg_ids,
-                         int n_seg, int max_seqlen_q, int Hq, int Hkv, int D,
+                         int n_seg, int max_seqlen_q, int max_seqlen_k, int Hq, int Hkv, int D,
                          int64_t q_stride_tok, int64_t k_stride_tok, int64_t v_stride_tok,
                          int64_t o_stride_tok, float softmax_scale, void* stream);
 

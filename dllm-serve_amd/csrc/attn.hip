@@ -571,6 +571,297 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WK == 1 ? 2
   }
 }
 
+// ---------------------------------------------------------------------------
+// K3a, dense varlen attention: K and V tiles go HBM -> LDS by buffer DMA
+// (buffer_load_dwordx4 ... lds, no VGPR staging); the V^T MFMA operand is
+// read with the transposing LDS read ds_read_b64_tr_b16.
+//
+// LDS per stage (2 stages): K [64 keys][256 B] then V [64 keys][256 B], no
+// padding; 16-byte chunks are XOR-swizzled inside a row so the MFMA operand
+// reads are bank-conflict free:
+//   K: physical chunk = logical chunk ^ (row & 15)
+//   V: physical chunk = logical chunk ^ (4 * (row & 3))
+// One DMA instruction writes 1 KiB = 4 rows; lane L of it carries row
+// 4q + L/16, physical chunk L%16.
+//
+// ds_read_b64_tr_b16 (gfx950): in each group of 16 lanes, lane 4k+c supplies
+// 8 bytes = elements [4c, 4c+4) of row k of a 4 x 16 block; lane n receives
+// column n (rows 0..3).  With rows = keys and columns = head-dim positions
+// this yields 4 consecutive keys of one d: half of a V^T A-operand fragment.
+constexpr int DK_TILE = 64;                    // keys per tile
+constexpr int DK_STAGE_BYTES = 2 * DK_TILE * 256;  // K + V
+
+// s_waitcnt vmcnt(N), expcnt / lgkmcnt untouched (gfx9 encoding: vmcnt bits
+// [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8]).
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
+}
+
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint8_t* lds_dst, uint32_t voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_dst, 16, (int)voff, 0, 0, 0);
+}
+
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ u32x2_t ds_read_tr16(const uint8_t* p) {
+  const i16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) i16x4_t*)(const_cast<uint8_t*>(p)));
+  return __builtin_bit_cast(u32x2_t, v);
+}
+
+// Per-lane LDS / DMA offsets.  The swizzles make every per-kk (K) and per-db
+// (V) read offset a XOR of one base with a compile-time constant:
+//   K read, kk:  lrow*256 + ((2kk + hl) ^ (lrow & 15))*16 = kbase ^ (32 kk)
+//   V read, db:  (4hl + k)*256 + (4(db ^ k) + 2 dhalf + c/2)*16 + 8(c&1) = vbase ^ (64 db)
+// A DMA instruction q writes tile rows R = 4q + L/16 (L = lane), physical
+// chunk P = L % 16, i.e. global chunk P ^ (R & 15) (K) or P ^ 4(R & 3) (V):
+//   K: (L/16)*kS + ((P ^ (L/16)) * 16 ^ 64 (q & 3))      V: (L/16)*vS + (P ^ 4(L/16))*16
+struct DenseAddr {
+  uint32_t kbase, vbase;
+  uint32_t kdma, vdma;
+};
+
+__device__ __forceinline__ void dense_addr(DenseAddr& ad, int lane, uint32_t kS, uint32_t vS) {
+  const int rl = lane >> 4, P = lane & 15;
+  ad.kdma = (uint32_t)rl * kS + (uint32_t)((P ^ rl) * 16);
+  ad.vdma = (uint32_t)rl * vS + (uint32_t)((P ^ (4 * rl)) * 16);
+  const int lrow = lane & 31, hl = lane >> 5;
+  ad.kbase = (uint32_t)(lrow * 256 + ((hl ^ (lrow & 15)) * 16));
+  const int dhalf = (lane >> 4) & 1, k = (lane & 15) >> 2, c = lane & 3;
+  ad.vbase = (uint32_t)((4 * hl + k) * 256 + (4 * k + 2 * dhalf + (c >> 1)) * 16 + 8 * (c & 1));
+}
+
+// Softmax state of NQ query blocks (32 M rows each) of one wavefront.
+template <int NQ>
+struct DenseState {
+  f32x16_t oacc[NQ][4];
+  float m_run[NQ];
+  float l_run[NQ];
+};
+
+// Online-softmax update of one query block from its two S^T key blocks;
+// returns the packed P^T fragments (B operands of O^T += V^T P^T).
+template <bool MASK>
+__device__ __forceinline__ void dense_softmax(f32x16_t (&sacc)[2], f32x16_t (&oacc)[4], float& m_run, float& l_run,
+                                              bf16x8_t (&pf)[4], float c, int k_valid, int hl) {
+  float mx = -INFINITY;
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      if (MASK) {
+        const int key = b * 32 + 8 * (i >> 2) + 4 * hl + (i & 3);
+        if (key >= k_valid) sacc[b][i] = -INFINITY;
+      }
+      mx = fmaxf(mx, sacc[b][i]);
+    }
+  mx = fmaxf(mx, __shfl_xor(mx, 32)) * c;
+  const bool need = mx > m_run + kLazy;
+  if (__builtin_amdgcn_ballot_w64(need)) {
+    const float m_new = need ? mx : m_run;
+    const float alpha = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
+    l_run *= alpha;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) oacc[db][i] *= alpha;
+    m_run = m_new;
+  }
+  const float neg_m = (m_run == -INFINITY) ? 0.f : -m_run;
+  float psum = 0.f;
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      u32x4_t pk;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[b][8 * j + 2 * w], c, neg_m));
+        const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[b][8 * j + 2 * w + 1], c, neg_m));
+        psum += p0 + p1;
+        pk[w] = cvt_pk_bf16(p0, p1);
+      }
+      pf[2 * b + j] = as_bf16x8(pk);
+    }
+  l_run += psum;
+}
+
+// One 64-key tile for one wavefront owning NQ query blocks: every K and V^T
+// operand fragment read from LDS feeds NQ MFMAs.
+template <int NQ, bool MASK>
+__device__ __forceinline__ void dense_tile(const uint8_t* Ks, const uint8_t* Vs, const DenseAddr& ad,
+                                           const bf16x8_t (&qf)[NQ][8], DenseState<NQ>& st, float c, int k_valid) {
+  const int lane = threadIdx.x & 63;
+  const int hl = lane >> 5;
+  // kk outer, key block inner: the 2*NQ accumulators form independent MFMA
+  // chains that interleave instead of one chain waiting on itself.
+  f32x16_t sacc[NQ][2];
+#pragma unroll
+  for (int q = 0; q < NQ; ++q)
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) sacc[q][b][i] = 0.f;
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk) {
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const bf16x8_t af =
+          as_bf16x8(*reinterpret_cast<const u32x4_t*>(Ks + b * 32 * 256 + (ad.kbase ^ (uint32_t)(32 * kk))));
+#pragma unroll
+      for (int q = 0; q < NQ; ++q)
+        sacc[q][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, qf[q][kk], sacc[q][b], 0, 0, 0);
+    }
+  }
+  bf16x8_t pf[NQ][4];
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) dense_softmax<MASK>(sacc[q], st.oacc[q], st.m_run[q], st.l_run[q], pf[q], c, k_valid, hl);
+  // key chunk outer, d block inner: 4*NQ independent accumulator chains.
+#pragma unroll
+  for (int cch = 0; cch < 4; ++cch) {
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      const uint8_t* vp = Vs + (ad.vbase ^ (uint32_t)(64 * db)) + cch * 16 * 256;
+      const u32x2_t lo = ds_read_tr16(vp);
+      const u32x2_t hi = ds_read_tr16(vp + 8 * 256);
+      u32x4_t a4 = {lo[0], lo[1], hi[0], hi[1]};
+      const bf16x8_t af = as_bf16x8(a4);
+#pragma unroll
+      for (int q = 0; q < NQ; ++q)
+        st.oacc[q][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, pf[q][cch], st.oacc[q][db], 0, 0, 0);
+    }
+  }
+}
+
+// NW wavefronts x NQ query blocks of 32 M rows = 32*NW*NQ rows per
+// workgroup; ST LDS stages (ST-1 tiles in flight while one is computed).
+template <int NW, int NQ, int ST>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NQ == 1 ? 2 : 1, NQ == 1 ? 2 : 1))) void attn_dense_kernel(AttnArgs a) {
+  constexpr int BM = 32 * NW * NQ;
+  constexpr int DMA_PER_WAVE = DK_TILE * 256 / 1024 / NW;  // 1 KiB DMA instructions per wave, K (same for V)
+  constexpr int DMA_TILE = 2 * DMA_PER_WAVE;               // this wave's DMA instructions per tile
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const int L = xcd_remap(blockIdx.x, gridDim.x);
+  if (L >= a.logical_blocks) return;
+  int r = L;
+  const int mt = r % a.mtiles;
+  r /= a.mtiles;
+  const int hkv = r % a.Hkv;
+  const int s = r / a.Hkv;
+  const int sid = a.seg_ids ? a.seg_ids[s] : s;
+  const int qrow0 = a.cu_q[sid];
+  const int Lq = a.cu_q[sid + 1] - qrow0;
+  const int krow0 = a.cu_k[sid];
+  const int Lk = a.cu_k[sid + 1] - krow0;
+  const int g = a.g;
+  const int M = Lq * g;
+  const int m_base = mt * BM;
+  if (m_base >= M) return;
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
+  const int lane = tid & 63;
+  const int lrow = lane & 31;
+  const int hl = lane >> 5;
+
+  const uint32_t kS = (uint32_t)(a.k_stride * 2), vS = (uint32_t)(a.v_stride * 2);
+  const __amdgpu_buffer_rsrc_t krs =
+      make_rsrc(a.k + (int64_t)krow0 * a.k_stride + hkv * HD, Lk > 0 ? (uint32_t)(Lk - 1) * kS + HD * 2 : 0u);
+  const __amdgpu_buffer_rsrc_t vrs =
+      make_rsrc(a.v + (int64_t)krow0 * a.v_stride + hkv * HD, Lk > 0 ? (uint32_t)(Lk - 1) * vS + HD * 2 : 0u);
+  DenseAddr ad;
+  dense_addr(ad, lane, kS, vS);
+
+  // DMA instruction j (global index q = DMA_PER_WAVE*wave + j) covers tile rows 4q..4q+3.
+  auto issue = [&](uint8_t* stage, int k0) {
+#pragma unroll
+    for (int j = 0; j < DMA_PER_WAVE; ++j) {
+      const int q = DMA_PER_WAVE * wave + j;
+      const uint32_t row = (uint32_t)(k0 + 4 * q);
+      dma16(krs, stage + q * 1024, row * kS + (ad.kdma ^ (uint32_t)(64 * (q & 3))));
+      dma16(vrs, stage + DK_TILE * 256 + q * 1024, row * vS + ad.vdma);
+    }
+  };
+
+  const int ntiles = (Lk + DK_TILE - 1) / DK_TILE;
+#pragma unroll
+  for (int j = 0; j < ST - 1; ++j)
+    if (j < ntiles) issue(lds + j * DK_STAGE_BYTES, j * DK_TILE);
+
+  // Q^T fragments; rows past the segment read as zero through the buffer bound.
+  bf16x8_t qf[NQ][8];
+  int tokq[NQ], headq[NQ];
+  bool okq[NQ];
+  {
+    const uint32_t qS = (uint32_t)(a.q_stride * 2);
+    const uint32_t qbytes = Lq > 0 ? (uint32_t)Lq * qS : 0u;
+    const __amdgpu_buffer_rsrc_t qrs = make_rsrc(a.q + (int64_t)qrow0 * a.q_stride, qbytes);
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const int m = m_base + (wave * NQ + q) * 32 + lrow;
+      okq[q] = m < M;
+      tokq[q] = okq[q] ? m / g : 0;
+      headq[q] = hkv * g + (okq[q] ? m - tokq[q] * g : 0);
+      const uint32_t qoff = okq[q] ? (uint32_t)tokq[q] * qS + (uint32_t)(headq[q] * HD + hl * 8) * 2u : qbytes;
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) qf[q][kk] = as_bf16x8(bload(qrs, qoff + (uint32_t)kk * 32u, 0u));
+    }
+  }
+
+  DenseState<NQ> st;
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) st.oacc[q][db][i] = 0.f;
+    st.m_run[q] = -INFINITY;
+    st.l_run[q] = 0.f;
+  }
+  const float c = a.scale_log2;
+
+  // Full tiles, the next tile's DMA in flight; the last tile is peeled off
+  // (masked) so the loop body holds a single tile variant.
+  // Tile t lives in stage t % ST.  At the top of iteration t this wave's DMA
+  // of tiles t+1 .. t+ST-2 may still be in flight (ST-2 tiles of DMA_TILE
+  // instructions); the barrier then makes everyone's DMA of tile t visible
+  // and frees stage (t-1) % ST, which receives tile t+ST-1.
+  for (int t = 0; t + 1 < ntiles; ++t) {
+    if (t + ST - 2 < ntiles) vm_wait<(ST - 2) * DMA_TILE>(); else vm_wait<0>();
+    __syncthreads();
+    uint8_t* cur = lds + (t % ST) * DK_STAGE_BYTES;
+    if (t + ST - 1 < ntiles) issue(lds + ((t + ST - 1) % ST) * DK_STAGE_BYTES, (t + ST - 1) * DK_TILE);
+    dense_tile<NQ, false>(cur, cur + DK_TILE * 256, ad, qf, st, c, DK_TILE);
+  }
+  if (ntiles > 0) {
+    const int t = ntiles - 1;
+    vm_wait<0>();
+    __syncthreads();
+    uint8_t* cur = lds + (t % ST) * DK_STAGE_BYTES;
+    dense_tile<NQ, true>(cur, cur + DK_TILE * 256, ad, qf, st, c, Lk - t * DK_TILE);
+  }
+
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    const float l_tot = st.l_run[q] + __shfl_xor(st.l_run[q], 32);
+    if (okq[q]) {
+      const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+      uint16_t* op = a.o + (int64_t)(qrow0 + tokq[q]) * a.o_stride + headq[q] * HD;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int rq = 0; rq < 4; ++rq) {
+          const int d = db * 32 + 8 * rq + 4 * hl;
+          u32x2_t w;
+          w[0] = cvt_pk_bf16(st.oacc[q][db][4 * rq + 0] * inv, st.oacc[q][db][4 * rq + 1] * inv);
+          w[1] = cvt_pk_bf16(st.oacc[q][db][4 * rq + 2] * inv, st.oacc[q][db][4 * rq + 3] * inv);
+          *reinterpret_cast<u32x2_t*>(op + d) = w;
+        }
+    }
+  }
+}
+
 // Merge the n_split partial records of every (segment, head, M row).
 // grid: (n_seg*Hkv*mtiles*32) rows / 2 per block; block 256 = 2 rows x 128 d.
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
@@ -611,8 +902,11 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
 
 static const float kLog2e = 1.4426950408889634f;
 
-// K3a: WM=4 wavefronts x 32 M rows, 64-key tiles (2 key blocks per wavefront).
-using DenseCfg = Cfg<4, 1, 2>;
+// K3a launch shapes (one query block of 32 rows per wavefront, two LDS
+// stages): 4 wavefronts (128 M rows) for short segments, 8 wavefronts
+// (256 M rows sharing each K/V tile) once a segment has >= 1024 M rows.
+constexpr int DENSE_ST = 2;
+constexpr int DENSE_LONG_M = 1024;
 // K3b: 1 x 32 M rows, 128-key tiles split over 4 wavefronts.
 using CachedCfg = Cfg<1, 4, 1>;
 
@@ -631,10 +925,24 @@ static int common_checks(const char* name, const void* q, const void* k, const v
   return DLLM_OK;
 }
 
+// Raise a kernel's dynamic-LDS limit (once per kernel and device).
 template <typename KernelFn>
 static int set_lds(KernelFn fn, int bytes, const char* name) {
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  static thread_local const void* done[16];
+  static thread_local int done_dev[16];
+  static thread_local int n_done = 0;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = -1;
+  const void* key = reinterpret_cast<const void*>(fn);
+  for (int i = 0; i < n_done; ++i)
+    if (done[i] == key && done_dev[i] == dev) return DLLM_OK;
+  hipError_t e = hipFuncSetAttribute(key, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
   if (e != hipSuccess) return fail(DLLM_ERR_HIP, "%s: hipFuncSetAttribute(LDS %d B): %s", name, bytes, hipGetErrorString(e));
+  if (n_done < 16) {
+    done[n_done] = key;
+    done_dev[n_done] = dev;
+    ++n_done;
+  }
   return DLLM_OK;
 }
 
@@ -666,16 +974,20 @@ extern "C" int dllm_attn_varlen_fwd(const dllm_bf16* q, const dllm_bf16* k, cons
   a.cu_q = cu_q; a.cu_k = cu_k; a.seg_ids = seg_ids;
   a.q_stride = q_stride_tok; a.k_stride = k_stride_tok; a.v_stride = v_stride_tok; a.o_stride = o_stride_tok;
   a.n_seg = n_seg; a.Hkv = Hkv; a.g = Hq / Hkv;
-  a.mtiles = (int)(((int64_t)max_seqlen_q * a.g + DenseCfg::BM - 1) / DenseCfg::BM);
+  const bool wide = (int64_t)max_seqlen_q * a.g >= DENSE_LONG_M;
+  const int nw = wide ? 8 : 4;
+  const int bm = 32 * nw;
+  a.mtiles = (int)(((int64_t)max_seqlen_q * a.g + bm - 1) / bm);
   a.n_split = 1;
   const int64_t logical = (int64_t)a.mtiles * Hkv * n_seg;
   if (logical > (int64_t)1 << 30) return fail(DLLM_ERR_INVALID_ARG, "%s: problem too large", name);
   a.logical_blocks = (int)logical;
   a.scale_log2 = softmax_scale * kLog2e;
-  auto kern = attn_fwd_kernel<4, 1, 2, false>;
-  if ((rc = set_lds(kern, DenseCfg::LDS_BYTES, name))) return rc;
+  auto kern = wide ? attn_dense_kernel<8, 1, DENSE_ST> : attn_dense_kernel<4, 1, DENSE_ST>;
+  constexpr int lds_bytes = DENSE_ST * DK_STAGE_BYTES;
+  if ((rc = set_lds(kern, lds_bytes, name))) return rc;
   const int nb = (int)((logical + 7) / 8 * 8);
-  kern<<<dim3(nb), dim3(256), DenseCfg::LDS_BYTES, reinterpret_cast<hipStream_t>(stream)>>>(a);
+  kern<<<dim3(nb), dim3(64 * nw), lds_bytes, reinterpret_cast<hipStream_t>(stream)>>>(a);
   return check_launch(name);
 }
 

@@ -110,7 +110,11 @@ class StepPlan:
                 spans.append((bs, bl))
                 keeps.append(keep_count(N - bl, st.retention_ratio))
             elif st.should_reuse_cache:
-                bs, bl = st.block_span(seq.num_prompt_tokens, N)
+                bs, bl_raw = st.compute_block_boundaries(seq.num_prompt_tokens, N)
+                if bl_raw < 0:  # the reference's torch.arange(bs, bs + bl) raises here too
+                    raise RuntimeError(f"sequence {seq.seq_id}: block {st.current_block_idx} starts at {bs}, "
+                                       f"past the {N} tokens of the sequence")
+                bl = bl_raw
                 modes.append(2)
                 rows.append(bl)
                 spans.append((bs, bl))

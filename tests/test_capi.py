@@ -1,0 +1,79 @@
+"""The C ABI library loads on the host, exports every entry point that
+include/dllm_attn.h declares with the arity the ctypes binding uses, and
+rejects invalid requests before touching the GPU (no kernel is launched)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from dllm_serve_amd import _capi
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "dllm_attn.h")
+
+
+def _declarations():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    decls = {}
+    for m in re.finditer(r"\b(dllm_\w+)\s*\(([^;{]*?)\)\s*;", text, flags=re.S):
+        params = m.group(2).strip()
+        decls[m.group(1)] = 0 if params in ("", "void") else params.count(",") + 1
+    return decls
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _capi.load()
+    decls = _declarations()
+    assert len(decls) >= 9
+    for name, arity in decls.items():
+        assert hasattr(lib, name), name
+        assert name in _capi.SIGNATURES, name
+        assert len(_capi.SIGNATURES[name][1]) == arity, (name, arity)
+    assert lib.dllm_abi_version() >= 100
+
+
+def test_workspace_size_functions():
+    # one split: no workspace; few long segments: split over keys
+    assert _capi.block_cached_workspace_size(1024, 32, 4000, 32, 32, 128) == 0
+    ws = _capi.block_cached_workspace_size(4, 64, 672, 32, 32, 128)
+    assert ws > 0 and ws % 4 == 0
+    assert _capi.select_workspace_size(4, 1216, 32, 32, 128, True) >= 4 * 32 * 128 * 2 + 4 * 32 * 1216 * 2
+    assert _capi.select_workspace_size(0, 10, 32, 32, 128, True) == 0
+
+
+def _err(rc):
+    return rc, _capi.load().dllm_last_error().decode()
+
+
+def test_argument_validation_without_gpu():
+    lib = _capi.load()
+    P = ctypes.c_void_p
+    fake = P(4096)  # never dereferenced: every call below fails validation first
+    rc, msg = _err(lib.dllm_attn_varlen_fwd(fake, fake, fake, fake, fake, fake, None, 1, 8, 8, 4, 4, 64,
+                                            256, 256, 256, 256, 0.125, None))
+    assert rc == _capi.DLLM_ERR_UNSUPPORTED and "head_dim" in msg
+    rc, msg = _err(lib.dllm_attn_varlen_fwd(fake, fake, fake, fake, fake, fake, None, 1, 8, 8, 6, 4, 128,
+                                            768, 512, 512, 768, 0.1, None))
+    assert rc == _capi.DLLM_ERR_INVALID_ARG and "multiple" in msg
+    rc, msg = _err(lib.dllm_attn_varlen_fwd(P(4098), fake, fake, fake, fake, fake, None, 1, 8, 8, 4, 4, 128,
+                                            512, 512, 512, 512, 0.1, None))
+    assert rc == _capi.DLLM_ERR_INVALID_ARG and "aligned" in msg
+    assert lib.dllm_attn_varlen_fwd(fake, fake, fake, fake, fake, fake, None, 0, 8, 8, 4, 4, 128,
+                                    512, 512, 512, 512, 0.1, None) == 0   # nothing to do
+    rc, msg = _err(lib.dllm_attn_block_cached_fwd(fake, fake, fake, fake, fake, None, 4, 64, 672, fake, fake,
+                                                  4096, fake, fake, 32, 32, 128, 4096, 4096, 4096, 4096, 0.1,
+                                                  None, 0, None))
+    assert rc == _capi.DLLM_ERR_WORKSPACE
+    rc, msg = _err(lib.dllm_select_kv_store(fake, fake, fake, 4096, 4096, 4096, fake, 1, 9000, 100, 64, 32, 32,
+                                            128, 1, 3, 11.3, fake, fake, 4096, fake, None, fake, 1 << 20, None))
+    assert rc == _capi.DLLM_ERR_UNSUPPORTED and "8192" in msg
+    rc, msg = _err(lib.dllm_store_kvcache(None, 4096, None, 4096, None, None, 10, None, 3, 4096, None))
+    assert rc == _capi.DLLM_ERR_INVALID_ARG
+    assert lib.dllm_store_kvcache(None, 4096, None, 4096, None, None, 10, None, 0, 4096, None) == 0
+
+
+def test_missing_library_fails_loudly(tmp_path, monkeypatch):
+    monkeypatch.setattr(_capi, "_lib", None)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        _capi.load(str(tmp_path / "absent.so"))

@@ -221,6 +221,159 @@ def bench_sparse_c4(dev, steps_block=64, quick=False):
                 speedup_vs_dense=ms_dense / ms_sparse, speedup_vs_ret1=ms_cached_full / ms_sparse)
 
 
+# ---------------------------------------------------------------------------
+# Full-model denoising driver (LLaDA-8B architecture, random N(0, 0.02)
+# weights): the caller of the attention path, used to report denoise-step
+# tokens/s = B * gen_length / total denoise time (the reference's formula,
+# tests/unit/test_llada_sparse.py:56).  Layer structure as
+# dllmserve/models/llada.py:61-97; low-confidence remasking as
+# dllmserve/engine/model_runner.py:756-949 (temperature 0).
+LLADA_8B = dict(layers=32, hidden=4096, heads=32, head_dim=128, mlp=12288, vocab=126464, eps=1e-5,
+                theta=500000.0, mask_id=126336)
+
+
+class LLaDA8B:
+    def __init__(self, dev, cfg=LLADA_8B, seed=0):
+        from dllm_serve_amd.layers.attention import Attention
+
+        g = torch.Generator(device=dev).manual_seed(seed)
+        H, F, V = cfg["hidden"], cfg["mlp"], cfg["vocab"]
+
+        def w(*shape):
+            return (torch.randn(*shape, generator=g, device=dev, dtype=torch.bfloat16) * 0.02)
+
+        self.cfg = cfg
+        self.dev = dev
+        self.wte = w(V, H)
+        self.lm_head = w(V, H)
+        self.layers = []
+        for _ in range(cfg["layers"]):
+            self.layers.append(dict(qkv=w(3 * H, H), o=w(H, H), gate_up=w(2 * F, H), down=w(H, F),
+                                    attn_norm=torch.ones(H, device=dev, dtype=torch.bfloat16),
+                                    ff_norm=torch.ones(H, device=dev, dtype=torch.bfloat16)))
+        self.ln_f = torch.ones(H, device=dev, dtype=torch.bfloat16)
+        self.attn = [Attention(cfg["heads"], cfg["head_dim"], cfg["head_dim"] ** -0.5, cfg["heads"], causal=False)
+                     for _ in range(cfg["layers"])]
+        D = cfg["head_dim"]
+        inv_freq = 1.0 / (cfg["theta"] ** (torch.arange(0, D, 2, dtype=torch.float32, device=dev) / D))
+        t = torch.arange(8192, dtype=torch.float32, device=dev)
+        f = torch.outer(t, inv_freq)
+        self.cos, self.sin = f.cos(), f.sin()
+
+    def bind_cache(self, num_pages):
+        c = self.cfg
+        self.kv = torch.zeros(2, c["layers"], num_pages, 256, c["heads"], c["head_dim"], dtype=torch.bfloat16,
+                              device=self.dev)
+        for i, a in enumerate(self.attn):
+            a.k_cache, a.v_cache = self.kv[0, i], self.kv[1, i]
+
+    def _rms(self, x, w):
+        xf = x.float()
+        return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.cfg["eps"])).to(x.dtype) * w
+
+    def _rope(self, x, pos):
+        cos, sin = self.cos[pos].unsqueeze(1), self.sin[pos].unsqueeze(1)
+        x1, x2 = x.float().chunk(2, dim=-1)
+        return torch.cat((x1 * cos - x2 * sin, x2 * cos + x1 * sin), dim=-1).to(x.dtype)
+
+    def forward(self, ids, pos):
+        c = self.cfg
+        H, nh, D = c["hidden"], c["heads"], c["head_dim"]
+        n = ids.shape[0]
+        h = self.wte[ids]
+        for L, a in zip(self.layers, self.attn):
+            x = self._rms(h, L["attn_norm"])
+            qkv = x @ L["qkv"].t()
+            q = self._rope(qkv[:, :H].view(n, nh, D), pos)
+            k = self._rope(qkv[:, H:2 * H].view(n, nh, D), pos)
+            v = qkv[:, 2 * H:].view(n, nh, D)
+            h = h + a(q, k, v) @ L["o"].t()
+            x = self._rms(h, L["ff_norm"])
+            gu = x @ L["gate_up"].t()
+            h = h + (torch.nn.functional.silu(gu[:, :c["mlp"]]) * gu[:, c["mlp"]:]) @ L["down"].t()
+        return self._rms(h, self.ln_f)
+
+
+def denoise(model, batch, prompt, gen, steps, block, sparse, dev, seed=0):
+    """Generate `gen` tokens for `batch` random prompts; returns (seconds, steps).
+
+    Token ids stay on the device; each step unmasks ceil(masked / remaining
+    steps) positions per sequence (over all generated rows when dense, over
+    the current block when cached), picked by confidence = max softmax prob."""
+    from dllm_serve_amd.engine.sequence import PageAllocator, Sequence, prepare_step
+    from dllm_serve_amd.sparse.state import SparseConfig
+    from dllm_serve_amd.utils.context import reset_context
+
+    c = model.cfg
+    g = torch.Generator().manual_seed(seed)
+    cfg = SparseConfig(enabled=True, default_block_len=block, retention_ratio=1.0, pool_kernel=3, delay_step=1,
+                       head_select=True) if sparse else None
+    seqs = [Sequence(torch.randint(0, c["mask_id"], (prompt,), generator=g).tolist(), gen, c["mask_id"], cfg,
+                     device=dev, steps=steps) for _ in range(batch)]
+    if sparse:
+        pages = sum(s.num_blocks for s in seqs)
+        model.bind_cache(pages)
+        alloc = PageAllocator(range(pages))
+        for s in seqs:
+            alloc.allocate(s)
+    tok = torch.tensor([s.token_ids for s in seqs], dtype=torch.int64, device=dev)  # [B, N]
+    n_masked = [gen] * batch          # masked rows left in the denoising window (host bookkeeping)
+    block_seen = [0] * batch
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        rows = [s.step_rows() for s in seqs]
+        ids = torch.cat([tok[i, a:a + n] for i, (a, n) in enumerate(rows)])
+        pos = torch.cat([torch.arange(a, a + n, device=dev) for a, n in rows])
+        prepare_step(seqs, dev, build_inputs=False)  # Context: cu_seqlens, slot lists, seqs
+        hidden = model.forward(ids, pos)
+        reset_context()
+        spans, off = [], 0
+        for i, (s, (a, n)) in enumerate(zip(seqs, rows)):
+            if s.sparse_state is None:
+                lo, hi, remain = s.num_prompt_tokens, s.num_tokens, s.steps - s.current_step
+            else:
+                st = s.sparse_state
+                bs, bl = st.block_span(s.num_prompt_tokens, s.num_tokens)
+                if st.current_block_idx != block_seen[i] or s.current_step == 0:
+                    block_seen[i] = st.current_block_idx
+                    n_masked[i] = bl
+                lo, hi, remain = bs, bs + bl, max(1, bl - st.step_in_block)
+            k = min(-(-n_masked[i] // max(1, remain)), n_masked[i])
+            n_masked[i] -= k
+            spans.append((off + lo - a, off + hi - a, lo, hi, k))
+            off += n
+        sel = torch.cat([hidden[x0:x1] for x0, x1, _, _, _ in spans])
+        p, x0 = torch.softmax((sel @ model.lm_head.t()).float(), dim=-1).max(dim=-1)
+        o = 0
+        for i, (_, _, lo, hi, k) in enumerate(spans):
+            m = hi - lo
+            if k > 0:
+                masked = tok[i, lo:hi] == c["mask_id"]
+                conf = torch.where(masked, p[o:o + m], torch.full_like(p[o:o + m], -float("inf")))
+                top = torch.topk(conf, k).indices
+                tok[i, lo + top] = torch.where(masked[top], x0[o:o + m][top], tok[i, lo + top])
+            o += m
+        for s in seqs:
+            s.advance()
+    torch.cuda.synchronize()
+    return time.perf_counter() - t0, steps
+
+
+def bench_denoise(dev):
+    """C2: LLaDA-8B, B=8, prompt 256, gen 128, steps 128, block 32."""
+    model = LLaDA8B(dev)
+    out = {}
+    for name, sparse in (("cached_ret1", True), ("dense", False)):
+        denoise(model, 8, 256, 128, 4, 32, sparse, dev, seed=1)  # warm-up (kernels, allocator)
+        secs, steps = denoise(model, 8, 256, 128, 128, 32, sparse, dev)
+        out[name] = dict(seconds=round(secs, 3), steps=steps, tokens_per_s=round(8 * 128 / secs, 1),
+                         ms_per_step=round(secs / steps * 1e3, 3))
+    del model
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(lens, Hq, Hkv, D, budget_s=12.0):
     """Oracle (numpy fp32) attention of the headline step's layer calls on the
     host cores; bounded sample of whole layer calls."""
@@ -262,6 +415,24 @@ def profile_run(lens, Hq, Hkv, D, n_layers, dev):
         _capi.attn_varlen_fwd(q, k, v, o, cu, cu, None, len(lens), max(lens), D ** -0.5)
     torch.cuda.synchronize()
     log(f"profile run done: 3 x 256 MiB copies, {n_layers} attention launches")
+
+
+TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "attn_dense_kernel_llada_c2_8x384_counters.md")
+
+
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary (counters scaled by a plain 256 MiB copy), or None."""
+    try:
+        text = open(TRAFFIC_SUMMARY).read()
+    except OSError:
+        return None
+    if kernel not in text.splitlines()[0]:
+        return None
+    for line in text.splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":")[1].strip())
+    return None
 
 
 def main() -> None:
@@ -313,12 +484,16 @@ def main() -> None:
         log("C4: sparse vs dense attention per 64-step block")
         r4s = bench_sparse_c4(dev)
         extra["c4_head_sparse_per_block"] = {k: round(v, 3) for k, v in r4s.items()}
+    if not args.quick:
+        log("C2 full model: LLaDA-8B denoise, B=8, prompt 256, gen 128, 128 steps (cached and dense)")
+        extra["c2_denoise_llada8b"] = bench_denoise(dev)
     cpu = None
     if not args.quick:
         log("CPU baseline (oracle)")
         cpu = cpu_baseline(lens, Hq, Hkv, D)
         cpu["value"] = round(cpu["value"], 4)
     achieved = r["tflops_kernel"]
+    kernel_name = "attn_dense_kernel<4,1,2>"
     line = {
         "metric": METRIC,
         "value": round(r["tflops_step"], 2),
@@ -336,8 +511,9 @@ def main() -> None:
                                "(prompt 256 + gen 128), 32 heads x 128, non-causal varlen",
                    "global_batch": 8, "seq_len": 384, "layers": n_layers},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
-                     "kernel": "attn_dense_kernel<4,1,2>", "kernel_us": round(r["kernel_us"], 3),
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                     "traffic": measured_traffic(kernel_name),
+                     "kernel": kernel_name, "kernel_us": round(r["kernel_us"], 3),
                      "flops_per_launch": r["flops_per_call"], "algorithmic_bytes_per_launch": r["bytes_per_call"]},
         "cpu_baseline": cpu,
     }

@@ -129,8 +129,9 @@ class PageAllocator:
         seq.block_table.clear()
 
 
-def prepare_step(seqs: list[Sequence], device, block_size: int = 256):
-    """Build (input_ids, positions) for one forward and install the Context.
+def prepare_step(seqs: list[Sequence], device, block_size: int = 256, build_inputs: bool = True):
+    """Install the Context of one forward and (optionally) build its
+    (input_ids, positions) from the sequences' host token lists.
 
     Rows of a sequence are all its tokens for cache states 0/1 and only the
     current block for state 2; slot lists are given for states 1/2.
@@ -139,8 +140,9 @@ def prepare_step(seqs: list[Sequence], device, block_size: int = 256):
     for seq in seqs:
         st = seq.sparse_state
         start, n = seq.step_rows()
-        ids.extend(seq.token_ids[start:start + n])
-        pos.extend(range(start, start + n))
+        if build_inputs:
+            ids.extend(seq.token_ids[start:start + n])
+            pos.extend(range(start, start + n))
         lens.append(n)
         if st is None or st.is_full_attention:
             slot_mapping.append([])
@@ -153,5 +155,7 @@ def prepare_step(seqs: list[Sequence], device, block_size: int = 256):
     cu = cu.to(device)
     set_context(True, cu_seqlens_q=None, cu_seqlens_k=cu, max_seqlen_q=0,
                 max_seqlen_k=int(sum(lens)), slot_mapping=slot_mapping, is_diffusion=True, seqs=seqs)
+    if not build_inputs:
+        return None
     return (torch.tensor(ids, dtype=torch.int64, device=device),
             torch.tensor(pos, dtype=torch.int64, device=device))

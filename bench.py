@@ -294,7 +294,7 @@ class LLaDA8B:
         return self._rms(h, self.ln_f)
 
 
-def denoise(model, batch, prompt, gen, steps, block, sparse, dev, seed=0):
+def denoise(model, batch, prompt, gen, steps, block, sparse, dev, seed=0, ratio=1.0, head_select=True):
     """Generate `gen` tokens for `batch` random prompts; returns (seconds, steps).
 
     Token ids stay on the device; each step unmasks ceil(masked / remaining
@@ -306,8 +306,8 @@ def denoise(model, batch, prompt, gen, steps, block, sparse, dev, seed=0):
 
     c = model.cfg
     g = torch.Generator().manual_seed(seed)
-    cfg = SparseConfig(enabled=True, default_block_len=block, retention_ratio=1.0, pool_kernel=3, delay_step=1,
-                       head_select=True) if sparse else None
+    cfg = SparseConfig(enabled=True, default_block_len=block, retention_ratio=ratio, pool_kernel=3, delay_step=1,
+                       head_select=head_select) if sparse else None
     seqs = [Sequence(torch.randint(0, c["mask_id"], (prompt,), generator=g).tolist(), gen, c["mask_id"], cfg,
                      device=dev, steps=steps) for _ in range(batch)]
     if sparse:
@@ -369,6 +369,22 @@ def bench_denoise(dev):
         secs, steps = denoise(model, 8, 256, 128, 128, 32, sparse, dev)
         out[name] = dict(seconds=round(secs, 3), steps=steps, tokens_per_s=round(8 * 128 / secs, 1),
                          ms_per_step=round(secs / steps * 1e3, 3))
+    del model
+    torch.cuda.empty_cache()
+    return out
+
+
+def bench_denoise_c4(dev):
+    """C4: LLaDA-8B, B=4, prompt 1024, gen 256, block 64: one 64-step block,
+    head-sparse (retention 0.5, head_select, pool 3) vs dense recompute."""
+    model = LLaDA8B(dev)
+    out = {}
+    for name, sparse in (("head_sparse_r0.5", True), ("dense", False)):
+        denoise(model, 4, 1024, 256, 3, 64, sparse, dev, seed=1, ratio=0.5)  # warm-up
+        secs, steps = denoise(model, 4, 1024, 256, 64, 64, sparse, dev, ratio=0.5)
+        out[name] = dict(seconds=round(secs, 3), steps=steps, tokens_per_s=round(4 * 64 / secs, 1),
+                         ms_per_step=round(secs / steps * 1e3, 3))
+    out["speedup"] = round(out["dense"]["seconds"] / out["head_sparse_r0.5"]["seconds"], 2)
     del model
     torch.cuda.empty_cache()
     return out
@@ -487,6 +503,8 @@ def main() -> None:
     if not args.quick:
         log("C2 full model: LLaDA-8B denoise, B=8, prompt 256, gen 128, 128 steps (cached and dense)")
         extra["c2_denoise_llada8b"] = bench_denoise(dev)
+        log("C4 full model: LLaDA-8B, B=4, prompt 1024, gen 256, one 64-step block, head-sparse vs dense")
+        extra["c4_denoise_llada8b_one_block"] = bench_denoise_c4(dev)
     cpu = None
     if not args.quick:
         log("CPU baseline (oracle)")

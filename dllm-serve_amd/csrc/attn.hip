@@ -1,13 +1,13 @@
 // K3a / K3b: bidirectional attention on gfx950 bf16 MFMA.
 //
-// One kernel template serves both paths:
-//   * K3a (dense varlen, modes 0/1): a workgroup of 4 wavefronts owns 128
-//     "M rows" of one segment and one KV head and streams the segment's keys
-//     through LDS in tiles of 64; each wavefront owns 32 M rows.
-//   * K3b (generation block vs cached KV, mode 2): a workgroup owns 32 M
-//     rows; its 4 wavefronts split every 128-key tile (32 keys each) and are
-//     merged in LDS at the end; long key ranges are also split across
-//     workgroups (partials in a workspace, merged by attn_combine_kernel).
+//   * K3a attn_dense_kernel (dense varlen, cache states 0/1): a workgroup of
+//     NW wavefronts owns NW*32 "M rows" of one segment and one KV head and
+//     streams the segment's keys through LDS in tiles.
+//   * K3b attn_cached_kernel (generation block vs cached KV, state 2): a
+//     workgroup owns 32 M rows; each of its 4 wavefronts takes 32 keys of
+//     every 128-key tile and the four states are merged in LDS at the end;
+//     long key ranges are also split across workgroups (partials in a
+//     workspace, merged by attn_combine_kernel).
 //
 // "M rows" pack the Hq/Hkv query heads that share a KV head: M row m of a
 // segment is token m / g, query head hkv*g + m % g (g = Hq/Hkv), so every
@@ -21,8 +21,8 @@
 // O^T accumulator of an M row in the same lane, so P^T goes straight from
 // the S^T accumulator registers into the B operand of the second product.
 // The key order inside each group of 16 is permuted consistently in the V^T
-// LDS tile and in P^T (a contraction is invariant under a permutation of its
-// summation index), which makes every operand fetch one 16-byte LDS read.
+// operand and in P^T (a contraction is invariant under a permutation of its
+// summation index), which makes every operand fetch a single LDS read.
 #include "common.h"
 
 #include <math.h>
@@ -33,28 +33,6 @@ namespace dllm {
 
 constexpr int HD = 128;       // head dim handled by this build
 constexpr int KSTR = HD + 8;  // LDS row stride (elements) of the K tile: 272 B, conflict-free 16 B reads
-
-template <int WM, int WK, int KBW>
-struct Cfg {
-  static constexpr int NKT = 32 * KBW * WK;  // keys per workgroup tile
-  static constexpr int VSTR = NKT + 8;       // LDS row stride (elements) of the V^T tile
-  static constexpr int K_ELEMS = NKT * KSTR;
-  static constexpr int V_ELEMS = HD * VSTR;
-  static constexpr int BUF_ELEMS = K_ELEMS + V_ELEMS;
-  static constexpr int BM = 32 * WM;               // M rows per workgroup
-  static constexpr int KCH = NKT / 16;             // 16-byte K chunks per thread per tile
-  static constexpr int VGR = NKT / 64;             // (4 keys x 8 d) V groups per thread per tile
-  static constexpr int LDS_BYTES = 2 * BUF_ELEMS * 2;
-};
-
-struct SegDesc {
-  int qrow0;     // first q / o row of the segment
-  int Lq;        // q rows (tokens)
-  int krow0;     // first contiguous k / v row
-  int Lkb;       // contiguous k / v rows
-  int n_c;       // cached rows in front of the contiguous ones (K3b)
-  int slot_base; // offset of this segment's slots
-};
 
 struct AttnArgs {
   const uint16_t* q;
@@ -84,13 +62,6 @@ __device__ __forceinline__ int xcd_remap(int b, int nb) {
   return (b & 7) * per + (b >> 3);
 }
 
-__device__ __forceinline__ u32x4_t zero_unless(u32x4_t v, bool ok) {
-  u32x4_t r;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) r[i] = ok ? v[i] : 0u;
-  return r;
-}
-
 // Buffer resource over [base, base + bytes): loads at offsets >= bytes return
 // zero, which is how rows past the end of a segment read as zero without any
 // per-lane clamping.  The whole offset is passed in the VGPR operand (the
@@ -103,473 +74,11 @@ __device__ __forceinline__ u32x4_t bload(__amdgpu_buffer_rsrc_t r, uint32_t voff
   return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0));
 }
 
-// Where each thread's 16-byte pieces of a key tile go:
-//   K: rows (tid >> 4) + 16 i, chunk tid & 15               (i < KCH)
-//   V: 4 rows 4 kg + e of the 8-element column chunk dc      (i < VGR)
-//      with idx = tid + 256 i, kg = idx % (NKT/4), dc = idx / (NKT/4)
-template <int WM, int WK, int KBW>
-struct TileRegs {
-  using C = Cfg<WM, WK, KBW>;
-  u32x4_t kr[C::KCH];
-  u32x4_t vr[C::VGR][4];
-
-  __device__ __forceinline__ void store(uint16_t* buf) const {
-    const int tid = threadIdx.x;
-    uint16_t* Ks = buf;
-    uint16_t* Vt = buf + C::K_ELEMS;
-#pragma unroll
-    for (int i = 0; i < C::KCH; ++i) {
-      const int row = (tid >> 4) + 16 * i;
-      const int ch = tid & 15;
-      *reinterpret_cast<u32x4_t*>(Ks + row * KSTR + ch * 8) = kr[i];
-    }
-#pragma unroll
-    for (int i = 0; i < C::VGR; ++i) {
-      const int idx = tid + 256 * i;
-      const int kg = idx % (C::NKT / 4);
-      const int dc = idx / (C::NKT / 4);
-      const int j = kg & 3;
-      // Keys 4kg..4kg+3 sit at positions pos..pos+3 of the permuted order:
-      // inside a group of 16 keys, position 8h + i holds key 4h + (i%4) + 8(i/4).
-      const int pos = 16 * (kg >> 2) + 8 * (j & 1) + 4 * (j >> 1);
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {  // word w holds d = dc*8 + 2w (low half), 2w+1 (high half)
-        const uint32_t a0 = vr[i][0][w], a1 = vr[i][1][w], a2 = vr[i][2][w], a3 = vr[i][3][w];
-        u32x2_t lo, hi;
-        lo[0] = __builtin_amdgcn_perm(a1, a0, 0x05040100u);
-        lo[1] = __builtin_amdgcn_perm(a3, a2, 0x05040100u);
-        hi[0] = __builtin_amdgcn_perm(a1, a0, 0x07060302u);
-        hi[1] = __builtin_amdgcn_perm(a3, a2, 0x07060302u);
-        const int d = dc * 8 + 2 * w;
-        *reinterpret_cast<u32x2_t*>(Vt + d * C::VSTR + pos) = lo;
-        *reinterpret_cast<u32x2_t*>(Vt + (d + 1) * C::VSTR + pos) = hi;
-      }
-    }
-  }
-};
-
-// Dense segments: K/V rows are contiguous token rows of the segment.  All
-// address arithmetic is scalar except one 32-bit base offset per piece.
-template <int WM, int WK, int KBW>
-struct DenseLoader : TileRegs<WM, WK, KBW> {
-  using C = Cfg<WM, WK, KBW>;
-  __amdgpu_buffer_rsrc_t krs, vrs;
-  uint32_t kS, vS;               // token stride in bytes
-  uint32_t k_off;                // this thread's K piece offset for tile row 0
-  uint32_t v_off[C::VGR];        // this thread's V piece offsets for tile row 0
-
-  __device__ __forceinline__ void init(const AttnArgs& a, const SegDesc& sd, int hkv) {
-    const int tid = threadIdx.x;
-    kS = (uint32_t)(a.k_stride * 2);
-    vS = (uint32_t)(a.v_stride * 2);
-    const uint16_t* kb = a.k + (int64_t)sd.krow0 * a.k_stride + hkv * HD;
-    const uint16_t* vb = a.v + (int64_t)sd.krow0 * a.v_stride + hkv * HD;
-    const int Lk = sd.Lkb;
-    krs = make_rsrc(kb, Lk > 0 ? (uint32_t)(Lk - 1) * kS + HD * 2 : 0u);
-    vrs = make_rsrc(vb, Lk > 0 ? (uint32_t)(Lk - 1) * vS + HD * 2 : 0u);
-    k_off = (uint32_t)(tid >> 4) * kS + (uint32_t)(tid & 15) * 16u;
-#pragma unroll
-    for (int i = 0; i < C::VGR; ++i) {
-      const int idx = tid + 256 * i;
-      const int kg = idx % (C::NKT / 4);
-      const int dc = idx / (C::NKT / 4);
-      v_off[i] = (uint32_t)(kg * 4) * vS + (uint32_t)dc * 16u;
-    }
-  }
-
-  __device__ __forceinline__ void load(int k0) {
-#pragma unroll
-    for (int i = 0; i < C::KCH; ++i) this->kr[i] = bload(krs, k_off + (uint32_t)(k0 + 16 * i) * kS, 0u);
-#pragma unroll
-    for (int i = 0; i < C::VGR; ++i)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) this->vr[i][e] = bload(vrs, v_off[i] + (uint32_t)(k0 + e) * vS, 0u);
-  }
-};
-
-// Cached segments (mode 2): key index kidx < n_c reads cache row
-// slots[slot_base + kidx]; n_c <= kidx < n_c + Lkb reads block row kidx - n_c.
-// The slots of the next-but-one tile are fetched while the next tile's rows
-// are loaded, so no tile waits on its own slot indirection.
-template <int WM, int WK, int KBW>
-struct CachedLoader : TileRegs<WM, WK, KBW> {
-  using C = Cfg<WM, WK, KBW>;
-  const AttnArgs* ap;
-  const int32_t* sp;   // this segment's slots (a valid dummy when it has none)
-  int hkv, kend, n_c, krow0, Lkb;
-  int sk[C::KCH];      // slots of this thread's K rows of the pending tile
-  int sv[C::VGR][4];   // slots of this thread's V rows of the pending tile
-
-  __device__ __forceinline__ void init(const AttnArgs& a, const SegDesc& sd, int hkv_, int kend_) {
-    ap = &a;
-    hkv = hkv_;
-    kend = kend_;
-    n_c = sd.n_c;
-    krow0 = sd.krow0;
-    Lkb = sd.Lkb;
-    sp = n_c > 0 ? a.slots + sd.slot_base : a.slot_off;
-  }
-
-  // Slot of cached row kidx; the index is clamped into the segment's slot
-  // list so the (unconditional) load is always in bounds.
-  __device__ __forceinline__ int slot_at(int kidx) const { return sp[min(max(kidx, 0), max(n_c - 1, 0))]; }
-
-  __device__ __forceinline__ void fetch_slots(int k0) {
-    const int tid = threadIdx.x;
-#pragma unroll
-    for (int i = 0; i < C::KCH; ++i) sk[i] = slot_at(k0 + (tid >> 4) + 16 * i);
-#pragma unroll
-    for (int i = 0; i < C::VGR; ++i) {
-      const int kg = (tid + 256 * i) % (C::NKT / 4);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) sv[i][e] = slot_at(k0 + kg * 4 + e);
-    }
-  }
-
-  __device__ __forceinline__ u32x4_t row_piece(const uint16_t* cache, const uint16_t* blk, int64_t stride, int slot,
-                                               int kidx, int col) const {
-    const AttnArgs& a = *ap;
-    const bool in_range = kidx < kend;
-    const bool cached = kidx < n_c;
-    const bool slot_ok = slot >= 0 && (int64_t)slot < a.cache_slots;
-    const uint16_t* p;
-    if (cached)
-      p = cache + (int64_t)(slot_ok ? slot : 0) * (a.Hkv * HD) + hkv * HD;
-    else
-      p = blk + (int64_t)(krow0 + min(max(kidx - n_c, 0), Lkb - 1)) * stride + hkv * HD;
-    return zero_unless(ld128(p + col), in_range && (!cached || slot_ok));
-  }
-
-  __device__ __forceinline__ void load(int k0) {
-    const AttnArgs& a = *ap;
-    const int tid = threadIdx.x;
-#pragma unroll
-    for (int i = 0; i < C::KCH; ++i)
-      this->kr[i] = row_piece(a.k_cache, a.k, a.k_stride, sk[i], k0 + (tid >> 4) + 16 * i, (tid & 15) * 8);
-#pragma unroll
-    for (int i = 0; i < C::VGR; ++i) {
-      const int idx = tid + 256 * i;
-      const int kg = idx % (C::NKT / 4);
-      const int dc = idx / (C::NKT / 4);
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        this->vr[i][e] = row_piece(a.v_cache, a.v, a.v_stride, sv[i][e], k0 + kg * 4 + e, dc * 8);
-    }
-  }
-};
-
 // Running softmax state of one wavefront (M row = lane % 32).  The reference
 // maximum m_run (log2 domain) is only raised when a new score exceeds it by
 // more than kLazy, so most tiles skip rescaling O; probabilities then stay
 // below 2^kLazy, well inside the bf16 / fp32 range.
 constexpr float kLazy = 8.0f;
-
-template <int KBW>
-struct WaveState {
-  f32x16_t oacc[4];
-  float m_run;  // reference maximum, log2 domain
-  float l_run;  // this lane's half of the row sum
-};
-
-// One key tile for one wavefront: S^T = K Q^T, online softmax, O^T += V^T P^T.
-template <int WM, int WK, int KBW, bool MASK>
-__device__ __forceinline__ void tile_compute(const uint16_t* Ks, const uint16_t* Vt, const bf16x8_t (&qf)[8],
-                                             WaveState<KBW>& st, float c, int k_valid) {
-  using C = Cfg<WM, WK, KBW>;
-  const int lane = threadIdx.x & 63;
-  const int lrow = lane & 31;
-  const int hl = lane >> 5;
-  const int wk = (threadIdx.x >> 6) / WM;
-
-  f32x16_t sacc[KBW];
-#pragma unroll
-  for (int b = 0; b < KBW; ++b) {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) sacc[b][i] = 0.f;
-    const int kb = wk * KBW + b;
-    const uint16_t* kp = Ks + (kb * 32 + lrow) * KSTR + hl * 8;
-#pragma unroll
-    for (int kk = 0; kk < 8; ++kk) {
-      const bf16x8_t af = as_bf16x8(*reinterpret_cast<const u32x4_t*>(kp + kk * 16));
-      sacc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, qf[kk], sacc[b], 0, 0, 0);
-    }
-  }
-
-  float mx = -INFINITY;
-#pragma unroll
-  for (int b = 0; b < KBW; ++b) {
-    const int kb = wk * KBW + b;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      if (MASK) {
-        const int key = kb * 32 + 8 * (i >> 2) + 4 * hl + (i & 3);
-        if (key >= k_valid) sacc[b][i] = -INFINITY;
-      }
-      mx = fmaxf(mx, sacc[b][i]);
-    }
-  }
-  mx = fmaxf(mx, __shfl_xor(mx, 32)) * c;  // c > 0: scaling commutes with max
-  const bool need = mx > st.m_run + kLazy;
-  if (__builtin_amdgcn_ballot_w64(need)) {
-    const float m_new = need ? mx : st.m_run;
-    const float alpha = (st.m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(st.m_run - m_new);
-    st.l_run *= alpha;
-#pragma unroll
-    for (int db = 0; db < 4; ++db)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) st.oacc[db][i] *= alpha;
-    st.m_run = m_new;
-  }
-  const float neg_m = (st.m_run == -INFINITY) ? 0.f : -st.m_run;
-
-  float psum = 0.f;
-  bf16x8_t pf[2 * KBW];
-#pragma unroll
-  for (int b = 0; b < KBW; ++b) {
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      u32x4_t pk;
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[b][8 * j + 2 * w], c, neg_m));
-        const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[b][8 * j + 2 * w + 1], c, neg_m));
-        psum += p0 + p1;
-        pk[w] = cvt_pk_bf16(p0, p1);
-      }
-      pf[2 * b + j] = as_bf16x8(pk);
-    }
-  }
-  st.l_run += psum;
-
-#pragma unroll
-  for (int db = 0; db < 4; ++db) {
-    const uint16_t* vp = Vt + (db * 32 + lrow) * C::VSTR + wk * KBW * 32 + hl * 8;
-#pragma unroll
-    for (int cch = 0; cch < 2 * KBW; ++cch) {
-      const bf16x8_t af = as_bf16x8(*reinterpret_cast<const u32x4_t*>(vp + cch * 16));
-      st.oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, pf[cch], st.oacc[db], 0, 0, 0);
-    }
-  }
-}
-
-template <int WM, int WK, int KBW, bool CACHED>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WK == 1 ? 2 : 1, WK == 1 ? 2 : 1))) void attn_fwd_kernel(AttnArgs a) {
-  using C = Cfg<WM, WK, KBW>;
-  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
-
-  const int L = xcd_remap(blockIdx.x, gridDim.x);
-  if (L >= a.logical_blocks) return;
-
-  int r = L;
-  int split = 0;
-  if (CACHED) {
-    split = r % a.n_split;
-    r /= a.n_split;
-  }
-  const int mt = r % a.mtiles;
-  r /= a.mtiles;
-  const int hkv = r % a.Hkv;
-  const int s = r / a.Hkv;
-  const int sid = a.seg_ids ? a.seg_ids[s] : s;
-
-  SegDesc sd;
-  sd.qrow0 = a.cu_q[sid];
-  sd.Lq = a.cu_q[sid + 1] - sd.qrow0;
-  if (CACHED) {
-    sd.krow0 = sd.qrow0;
-    sd.Lkb = sd.Lq;
-    sd.slot_base = a.slot_off[s];
-    sd.n_c = a.slot_off[s + 1] - sd.slot_base;
-  } else {
-    sd.krow0 = a.cu_k[sid];
-    sd.Lkb = a.cu_k[sid + 1] - sd.krow0;
-    sd.n_c = 0;
-    sd.slot_base = 0;
-  }
-  const int g = a.g;
-  const int M = sd.Lq * g;
-  const int m_base = mt * C::BM;
-  if (m_base >= M) return;
-  const int Lk = sd.n_c + sd.Lkb;
-  int kbeg = 0, kend = Lk;
-  if (CACHED) {
-    kbeg = split * a.keys_per_split;
-    kend = min(Lk, kbeg + a.keys_per_split);
-    if (kbeg > kend) kbeg = kend;
-  }
-
-  const int tid = threadIdx.x;
-  const int wave = tid >> 6;
-  const int lane = tid & 63;
-  const int lrow = lane & 31;
-  const int hl = lane >> 5;
-  const int wm = wave % WM;
-  const int wk = wave / WM;
-
-  // ---- Q^T fragments (B operand of S^T = K Q^T), resident for the whole loop.
-  // Rows past the segment (M tail) read as zero through the buffer bound.
-  const int m = m_base + wm * 32 + lrow;
-  const bool m_ok = m < M;
-  const int tok = m_ok ? m / g : 0;
-  const int head = hkv * g + (m_ok ? m - tok * g : 0);
-  bf16x8_t qf[8];
-  {
-    const uint32_t qS = (uint32_t)(a.q_stride * 2);
-    const __amdgpu_buffer_rsrc_t qrs =
-        make_rsrc(a.q + (int64_t)sd.qrow0 * a.q_stride, sd.Lq > 0 ? (uint32_t)sd.Lq * qS : 0u);
-
-    const uint32_t qbytes = sd.Lq > 0 ? (uint32_t)sd.Lq * qS : 0u;
-    const uint32_t qoff = m_ok ? (uint32_t)tok * qS + (uint32_t)(head * HD + hl * 8) * 2u : qbytes;
-#pragma unroll
-    for (int kk = 0; kk < 8; ++kk) qf[kk] = as_bf16x8(bload(qrs, qoff + (uint32_t)kk * 32u, 0u));
-  }
-
-  WaveState<KBW> st;
-#pragma unroll
-  for (int db = 0; db < 4; ++db)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) st.oacc[db][i] = 0.f;
-  st.m_run = -INFINITY;
-  st.l_run = 0.f;
-  const float c = a.scale_log2;
-
-  const int ntiles = (kend - kbeg + C::NKT - 1) / C::NKT;
-  using Loader = typename std::conditional<CACHED, CachedLoader<WM, WK, KBW>, DenseLoader<WM, WK, KBW>>::type;
-  Loader io;
-  if constexpr (CACHED) {
-    io.init(a, sd, hkv, kend);
-    io.fetch_slots(kbeg);
-  } else {
-    io.init(a, sd, hkv);
-  }
-  if (ntiles > 0) {
-    io.load(kbeg);
-    if constexpr (CACHED) io.fetch_slots(kbeg + C::NKT);
-    io.store(smem);
-  }
-  __syncthreads();
-
-  // Full tiles with the next tile's loads in flight; the last (possibly
-  // partial) tile is peeled off and masked.
-  for (int t = 0; t + 1 < ntiles; ++t) {
-    const int k0 = kbeg + t * C::NKT;
-    io.load(k0 + C::NKT);
-    if constexpr (CACHED) io.fetch_slots(k0 + 2 * C::NKT);
-    const uint16_t* Ks = smem + (t & 1) * C::BUF_ELEMS;
-    tile_compute<WM, WK, KBW, false>(Ks, Ks + C::K_ELEMS, qf, st, c, C::NKT);
-    io.store(smem + ((t + 1) & 1) * C::BUF_ELEMS);
-    __syncthreads();
-  }
-  if (ntiles > 0) {
-    const int t = ntiles - 1;
-    const int k_valid = kend - (kbeg + t * C::NKT);
-    const uint16_t* Ks = smem + (t & 1) * C::BUF_ELEMS;
-    if (k_valid < C::NKT)
-      tile_compute<WM, WK, KBW, true>(Ks, Ks + C::K_ELEMS, qf, st, c, k_valid);
-    else
-      tile_compute<WM, WK, KBW, false>(Ks, Ks + C::K_ELEMS, qf, st, c, C::NKT);
-  }
-  __syncthreads();
-
-  const float m_run = st.m_run;
-  const float l_tot = st.l_run + __shfl_xor(st.l_run, 32);
-  f32x16_t (&oacc)[4] = st.oacc;
-
-  if constexpr (WK == 1) {
-    // ---- direct epilogue: normalise and store bf16
-    if (m_ok) {
-      const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-      uint16_t* op = a.o + (int64_t)(sd.qrow0 + tok) * a.o_stride + head * HD;
-#pragma unroll
-      for (int db = 0; db < 4; ++db)
-#pragma unroll
-        for (int rq = 0; rq < 4; ++rq) {
-          const int d = db * 32 + 8 * rq + 4 * hl;
-          u32x2_t w;
-          w[0] = pack_bf16x2(oacc[db][4 * rq + 0] * inv, oacc[db][4 * rq + 1] * inv);
-          w[1] = pack_bf16x2(oacc[db][4 * rq + 2] * inv, oacc[db][4 * rq + 3] * inv);
-          *reinterpret_cast<u32x2_t*>(op + d) = w;
-        }
-    }
-  } else {
-    // ---- merge the WK wavefronts' partial softmax states in LDS
-    float* red = reinterpret_cast<float*>(smem);
-    float* red_m = red;                 // [WK][32]
-    float* red_l = red + WK * 32;       // [WK][32]
-    float* ored = red + 2 * WK * 32;    // [WK][128][32]
-    if (hl == 0) {
-      red_m[wk * 32 + lrow] = m_run;
-      red_l[wk * 32 + lrow] = l_tot;
-    }
-    __syncthreads();
-    float m_all = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < WK; ++w) m_all = fmaxf(m_all, red_m[w * 32 + lrow]);
-    const float m_all_use = (m_all == -INFINITY) ? 0.f : m_all;
-    const float fac = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run - m_all_use);
-#pragma unroll
-    for (int db = 0; db < 4; ++db)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int d = db * 32 + 8 * (i >> 2) + 4 * hl + (i & 3);
-        ored[(wk * HD + d) * 32 + lrow] = oacc[db][i] * fac;
-      }
-    __syncthreads();
-    // 256 threads: row q = tid / 8, 16 consecutive d per thread.
-    const int q = tid >> 3;
-    const int d0 = (tid & 7) * 16;
-    float mq = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < WK; ++w) mq = fmaxf(mq, red_m[w * 32 + q]);
-    const float mq_use = (mq == -INFINITY) ? 0.f : mq;
-    float lq = 0.f;
-#pragma unroll
-    for (int w = 0; w < WK; ++w) {
-      const float mw = red_m[w * 32 + q];
-      lq += (mw == -INFINITY) ? 0.f : red_l[w * 32 + q] * __builtin_amdgcn_exp2f(mw - mq_use);
-    }
-    float acc[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      float sum = 0.f;
-#pragma unroll
-      for (int w = 0; w < WK; ++w) sum += ored[(w * HD + d0 + i) * 32 + q];
-      acc[i] = sum;
-    }
-    const int mrow = m_base + q;
-    if (mrow < M) {
-      const int tq = mrow / g;
-      const int hq = hkv * g + (mrow - tq * g);
-      if (a.n_split == 1) {
-        const float inv = lq > 0.f ? 1.f / lq : 0.f;
-        uint16_t* op = a.o + (int64_t)(sd.qrow0 + tq) * a.o_stride + hq * HD + d0;
-        u32x4_t w0, w1;
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          w0[w] = pack_bf16x2(acc[2 * w] * inv, acc[2 * w + 1] * inv);
-          w1[w] = pack_bf16x2(acc[8 + 2 * w] * inv, acc[8 + 2 * w + 1] * inv);
-        }
-        st128(op, w0);
-        st128(op + 8, w1);
-      } else {
-        // partial record P = ((s*Hkv + hkv)*mtiles + mt)*n_split + split, 32 rows each
-        const int64_t P = (((int64_t)s * a.Hkv + hkv) * a.mtiles + mt) * a.n_split + split;
-        float* po = a.ws + (P * 32 + q) * HD + d0;
-#pragma unroll
-        for (int i = 0; i < 16; i += 4) {
-          f32x4_t v4 = {acc[i], acc[i + 1], acc[i + 2], acc[i + 3]};
-          *reinterpret_cast<f32x4_t*>(po + i) = v4;
-        }
-        if ((tid & 7) == 0) {
-          const int64_t nrec = (int64_t)a.n_seg * a.Hkv * a.mtiles * a.n_split;
-          float* pml = a.ws + nrec * 32 * HD + (P * 32 + q) * 2;
-          pml[0] = mq;
-          pml[1] = lq;
-        }
-      }
-    }
-  }
-}
 
 // ---------------------------------------------------------------------------
 // K3a, dense varlen attention: K and V tiles go HBM -> LDS by buffer DMA
@@ -588,8 +97,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WK == 1 ? 2
 // 8 bytes = elements [4c, 4c+4) of row k of a 4 x 16 block; lane n receives
 // column n (rows 0..3).  With rows = keys and columns = head-dim positions
 // this yields 4 consecutive keys of one d: half of a V^T A-operand fragment.
-constexpr int DK_TILE = 64;                    // keys per tile
-constexpr int DK_STAGE_BYTES = 2 * DK_TILE * 256;  // K + V
 
 // s_waitcnt vmcnt(N), expcnt / lgkmcnt untouched (gfx9 encoding: vmcnt bits
 // [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8]).
@@ -642,17 +149,17 @@ struct DenseState {
 
 // Online-softmax update of one query block from its two S^T key blocks;
 // returns the packed P^T fragments (B operands of O^T += V^T P^T).
-template <bool MASK>
-__device__ __forceinline__ void dense_softmax(f32x16_t (&sacc)[2], f32x16_t (&oacc)[4], float& m_run, float& l_run,
-                                              bf16x8_t (&pf)[4], float c, int k_valid, int hl) {
+template <int KB, bool MASK>
+__device__ __forceinline__ void dense_softmax(f32x16_t (&sacc)[KB], f32x16_t (&oacc)[4], float& m_run, float& l_run,
+                                              bf16x8_t (&pf)[2 * KB], float c, int k_valid, uint64_t bad, int hl) {
   float mx = -INFINITY;
 #pragma unroll
-  for (int b = 0; b < 2; ++b)
+  for (int b = 0; b < KB; ++b)
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       if (MASK) {
         const int key = b * 32 + 8 * (i >> 2) + 4 * hl + (i & 3);
-        if (key >= k_valid) sacc[b][i] = -INFINITY;
+        if (key >= k_valid || ((bad >> key) & 1ull)) sacc[b][i] = -INFINITY;
       }
       mx = fmaxf(mx, sacc[b][i]);
     }
@@ -671,7 +178,7 @@ __device__ __forceinline__ void dense_softmax(f32x16_t (&sacc)[2], f32x16_t (&oa
   const float neg_m = (m_run == -INFINITY) ? 0.f : -m_run;
   float psum = 0.f;
 #pragma unroll
-  for (int b = 0; b < 2; ++b)
+  for (int b = 0; b < KB; ++b)
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       u32x4_t pk;
@@ -689,24 +196,26 @@ __device__ __forceinline__ void dense_softmax(f32x16_t (&sacc)[2], f32x16_t (&oa
 
 // One 64-key tile for one wavefront owning NQ query blocks: every K and V^T
 // operand fragment read from LDS feeds NQ MFMAs.
-template <int NQ, bool MASK>
+template <int NQ, int TK, bool MASK>
 __device__ __forceinline__ void dense_tile(const uint8_t* Ks, const uint8_t* Vs, const DenseAddr& ad,
-                                           const bf16x8_t (&qf)[NQ][8], DenseState<NQ>& st, float c, int k_valid) {
+                                           const bf16x8_t (&qf)[NQ][8], DenseState<NQ>& st, float c, int k_valid,
+                                           uint64_t bad = 0) {
+  constexpr int KB = TK / 32;  // key blocks of 32 per tile
   const int lane = threadIdx.x & 63;
   const int hl = lane >> 5;
-  // kk outer, key block inner: the 2*NQ accumulators form independent MFMA
+  // kk outer, key block inner: the KB*NQ accumulators form independent MFMA
   // chains that interleave instead of one chain waiting on itself.
-  f32x16_t sacc[NQ][2];
+  f32x16_t sacc[NQ][KB];
 #pragma unroll
   for (int q = 0; q < NQ; ++q)
 #pragma unroll
-    for (int b = 0; b < 2; ++b)
+    for (int b = 0; b < KB; ++b)
 #pragma unroll
       for (int i = 0; i < 16; ++i) sacc[q][b][i] = 0.f;
 #pragma unroll
   for (int kk = 0; kk < 8; ++kk) {
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
+    for (int b = 0; b < KB; ++b) {
       const bf16x8_t af =
           as_bf16x8(*reinterpret_cast<const u32x4_t*>(Ks + b * 32 * 256 + (ad.kbase ^ (uint32_t)(32 * kk))));
 #pragma unroll
@@ -714,12 +223,13 @@ __device__ __forceinline__ void dense_tile(const uint8_t* Ks, const uint8_t* Vs,
         sacc[q][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, qf[q][kk], sacc[q][b], 0, 0, 0);
     }
   }
-  bf16x8_t pf[NQ][4];
+  bf16x8_t pf[NQ][2 * KB];
 #pragma unroll
-  for (int q = 0; q < NQ; ++q) dense_softmax<MASK>(sacc[q], st.oacc[q], st.m_run[q], st.l_run[q], pf[q], c, k_valid, hl);
+  for (int q = 0; q < NQ; ++q)
+    dense_softmax<KB, MASK>(sacc[q], st.oacc[q], st.m_run[q], st.l_run[q], pf[q], c, k_valid, bad, hl);
   // key chunk outer, d block inner: 4*NQ independent accumulator chains.
 #pragma unroll
-  for (int cch = 0; cch < 4; ++cch) {
+  for (int cch = 0; cch < 2 * KB; ++cch) {
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
       const uint8_t* vp = Vs + (ad.vbase ^ (uint32_t)(64 * db)) + cch * 16 * 256;
@@ -736,11 +246,13 @@ __device__ __forceinline__ void dense_tile(const uint8_t* Ks, const uint8_t* Vs,
 
 // NW wavefronts x NQ query blocks of 32 M rows = 32*NW*NQ rows per
 // workgroup; ST LDS stages (ST-1 tiles in flight while one is computed).
-template <int NW, int NQ, int ST>
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NQ == 1 ? 2 : 1, NQ == 1 ? 2 : 1))) void attn_dense_kernel(AttnArgs a) {
+template <int NW, int NQ, int ST, int TK, int OCC>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void attn_dense_kernel(AttnArgs a) {
   constexpr int BM = 32 * NW * NQ;
-  constexpr int DMA_PER_WAVE = DK_TILE * 256 / 1024 / NW;  // 1 KiB DMA instructions per wave, K (same for V)
+  constexpr int STAGE = 2 * TK * 256;                      // K + V tile bytes
+  constexpr int DMA_PER_WAVE = TK * 256 / 1024 / NW;       // 1 KiB DMA instructions per wave, K (same for V)
   constexpr int DMA_TILE = 2 * DMA_PER_WAVE;               // this wave's DMA instructions per tile
+  static_assert(DMA_PER_WAVE >= 1 && TK % 32 == 0, "tile shape");
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int L = xcd_remap(blockIdx.x, gridDim.x);
   if (L >= a.logical_blocks) return;
@@ -780,14 +292,14 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NQ == 1
       const int q = DMA_PER_WAVE * wave + j;
       const uint32_t row = (uint32_t)(k0 + 4 * q);
       dma16(krs, stage + q * 1024, row * kS + (ad.kdma ^ (uint32_t)(64 * (q & 3))));
-      dma16(vrs, stage + DK_TILE * 256 + q * 1024, row * vS + ad.vdma);
+      dma16(vrs, stage + TK * 256 + q * 1024, row * vS + ad.vdma);
     }
   };
 
-  const int ntiles = (Lk + DK_TILE - 1) / DK_TILE;
+  const int ntiles = (Lk + TK - 1) / TK;
 #pragma unroll
   for (int j = 0; j < ST - 1; ++j)
-    if (j < ntiles) issue(lds + j * DK_STAGE_BYTES, j * DK_TILE);
+    if (j < ntiles) issue(lds + j * STAGE, j * TK);
 
   // Q^T fragments; rows past the segment read as zero through the buffer bound.
   bf16x8_t qf[NQ][8];
@@ -830,16 +342,16 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NQ == 1
   for (int t = 0; t + 1 < ntiles; ++t) {
     if (t + ST - 2 < ntiles) vm_wait<(ST - 2) * DMA_TILE>(); else vm_wait<0>();
     __syncthreads();
-    uint8_t* cur = lds + (t % ST) * DK_STAGE_BYTES;
-    if (t + ST - 1 < ntiles) issue(lds + ((t + ST - 1) % ST) * DK_STAGE_BYTES, (t + ST - 1) * DK_TILE);
-    dense_tile<NQ, false>(cur, cur + DK_TILE * 256, ad, qf, st, c, DK_TILE);
+    uint8_t* cur = lds + (t % ST) * STAGE;
+    if (t + ST - 1 < ntiles) issue(lds + ((t + ST - 1) % ST) * STAGE, (t + ST - 1) * TK);
+    dense_tile<NQ, TK, false>(cur, cur + TK * 256, ad, qf, st, c, TK);
   }
   if (ntiles > 0) {
     const int t = ntiles - 1;
     vm_wait<0>();
     __syncthreads();
-    uint8_t* cur = lds + (t % ST) * DK_STAGE_BYTES;
-    dense_tile<NQ, true>(cur, cur + DK_TILE * 256, ad, qf, st, c, Lk - t * DK_TILE);
+    uint8_t* cur = lds + (t % ST) * STAGE;
+    dense_tile<NQ, TK, true>(cur, cur + TK * 256, ad, qf, st, c, Lk - t * TK);
   }
 
 #pragma unroll
@@ -858,6 +370,241 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NQ == 1
           w[1] = cvt_pk_bf16(st.oacc[q][db][4 * rq + 2] * inv, st.oacc[q][db][4 * rq + 3] * inv);
           *reinterpret_cast<u32x2_t*>(op + d) = w;
         }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// K3b v2: block rows vs [cached rows (by slot) ; block rows], same DMA + swizzled
+// LDS tiles as K3a.  Tile = 128 keys; wavefront w DMAs tile rows 32w..32w+31
+// (8 K + 8 V instructions, per-lane 64-bit addresses so caches above 4 GiB work)
+// and computes exactly those 32 keys for the workgroup's 32 M rows; the four
+// wavefronts' softmax states are merged in LDS at the end.  A cached row whose
+// slot is outside the cache is excluded (masked) from the softmax.
+constexpr int CK_TILE = 128;
+constexpr int CK_STAGE = 2 * CK_TILE * 256;
+
+__device__ __forceinline__ void gdma16(const void* g, uint8_t* lds_dst) {
+  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds_dst, 16, 0, 0);
+}
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void attn_cached_kernel(AttnArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const int L = xcd_remap(blockIdx.x, gridDim.x);
+  if (L >= a.logical_blocks) return;
+  int r = L;
+  const int split = r % a.n_split;
+  r /= a.n_split;
+  const int mt = r % a.mtiles;
+  r /= a.mtiles;
+  const int hkv = r % a.Hkv;
+  const int s = r / a.Hkv;
+  const int sid = a.seg_ids ? a.seg_ids[s] : s;
+  const int qrow0 = a.cu_q[sid];
+  const int Lq = a.cu_q[sid + 1] - qrow0;
+  const int slot_base = a.slot_off[s];
+  const int n_c = a.slot_off[s + 1] - slot_base;
+  const int g = a.g;
+  const int M = Lq * g;
+  const int m_base = mt * 32;
+  if (m_base >= M) return;
+  const int Lk = n_c + Lq;
+  const int kbeg = min(split * a.keys_per_split, Lk);
+  const int kend = min(Lk, kbeg + a.keys_per_split);
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int lrow = lane & 31;
+  const int hl = lane >> 5;
+  const int rl = lane >> 4, P = lane & 15;
+
+  // ---- per-lane DMA geometry: instruction j of this wave covers tile rows
+  // 32 wave + 4j + rl; K chunk (P ^ rl) ^ 4(j & 3), V chunk P ^ 4 rl.
+  const uint32_t kchunk = (uint32_t)((P ^ rl) * 16);
+  const uint32_t vchunk = (uint32_t)((P ^ (4 * rl)) * 16);
+  const int64_t row_elems = (int64_t)a.Hkv * HD;
+  const int32_t* sp = n_c > 0 ? a.slots + slot_base : a.slot_off;  // a valid dummy when there are none
+  int slot_next[8];
+  uint32_t bad_next = 0;  // wave-uniform mask of this wave's rows (bit 4j + rl) with an invalid slot
+  auto fetch_slots = [&](int k0) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int kidx = k0 + 32 * wave + 4 * j + rl;
+      slot_next[j] = sp[min(max(kidx, 0), max(n_c - 1, 0))];
+    }
+  };
+  // Rows past kend read the last valid row; a cached row with an invalid
+  // slot reads block row 0 (never the cache, which may be absent).  Both are
+  // masked out of the softmax, so only the address needs to be valid.
+  auto issue = [&](uint8_t* stage, int k0) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int kidx = min(k0 + 32 * wave + 4 * j + rl, max(kend - 1, 0));
+      const int64_t sl = slot_next[j];
+      const bool cached = kidx < n_c;
+      const bool ok = sl >= 0 && sl < a.cache_slots;
+      const uint16_t* krow;
+      const uint16_t* vrow;
+      if (cached && ok) {
+        krow = a.k_cache + sl * row_elems + hkv * HD;
+        vrow = a.v_cache + sl * row_elems + hkv * HD;
+      } else {
+        const int64_t br = qrow0 + (cached ? 0 : kidx - n_c);
+        krow = a.k + br * a.k_stride + hkv * HD;
+        vrow = a.v + br * a.v_stride + hkv * HD;
+      }
+      const int q = 8 * wave + j;
+      gdma16(reinterpret_cast<const uint8_t*>(krow) + (kchunk ^ (uint32_t)(64 * (j & 3))), stage + q * 1024);
+      gdma16(reinterpret_cast<const uint8_t*>(vrow) + vchunk, stage + CK_TILE * 256 + q * 1024);
+    }
+  };
+  // rows of this wave's block whose slot is invalid, as a 32-bit mask (bit = 4j + rl)
+  auto invalid_rows = [&](int k0) -> uint32_t {
+    uint32_t m = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int kidx = k0 + 32 * wave + 4 * j + rl;
+      const int64_t sl = slot_next[j];
+      const bool bad = kidx < n_c && kidx < kend && (sl < 0 || sl >= a.cache_slots);
+      const uint64_t b = __builtin_amdgcn_ballot_w64(bad);
+      // lanes 16 rl' .. 16 rl' + 15 share row 4j + rl'
+#pragma unroll
+      for (int x = 0; x < 4; ++x)
+        if ((b >> (16 * x)) & 0xffffull) m |= 1u << (4 * j + x);
+    }
+    return m;
+  };
+
+  const int ntiles = (kend - kbeg + CK_TILE - 1) / CK_TILE;
+  uint32_t bad_cur = 0;
+  if (ntiles > 0) {
+    fetch_slots(kbeg);
+    bad_next = invalid_rows(kbeg);
+    issue(lds, kbeg);
+    bad_cur = bad_next;
+    if (ntiles > 1) fetch_slots(kbeg + CK_TILE);
+  }
+
+  // ---- Q^T fragments
+  const int m = m_base + lrow;
+  const bool m_ok = m < M;
+  const int tok = m_ok ? m / g : 0;
+  const int head = hkv * g + (m_ok ? m - tok * g : 0);
+  bf16x8_t qf[1][8];
+  {
+    const uint32_t qS = (uint32_t)(a.q_stride * 2);
+    const uint32_t qbytes = Lq > 0 ? (uint32_t)Lq * qS : 0u;
+    const __amdgpu_buffer_rsrc_t qrs = make_rsrc(a.q + (int64_t)qrow0 * a.q_stride, qbytes);
+    const uint32_t qoff = m_ok ? (uint32_t)tok * qS + (uint32_t)(head * HD + hl * 8) * 2u : qbytes;
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) qf[0][kk] = as_bf16x8(bload(qrs, qoff + (uint32_t)kk * 32u, 0u));
+  }
+  DenseAddr ad;
+  dense_addr(ad, lane, 0u, 0u);
+  DenseState<1> st;
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) st.oacc[0][db][i] = 0.f;
+  st.m_run[0] = -INFINITY;
+  st.l_run[0] = 0.f;
+  const float c = a.scale_log2;
+
+  for (int t = 0; t < ntiles; ++t) {
+    const int k0 = kbeg + t * CK_TILE;
+    vm_wait<0>();      // this lane's DMA of tile t (and the slots of tile t+1) have landed
+    __syncthreads();   // everyone's DMA of tile t is visible; stage (t+1)&1 is free
+    uint32_t bad_now = bad_cur;
+    if (t + 1 < ntiles) {
+      bad_next = invalid_rows(k0 + CK_TILE);
+      issue(lds + ((t + 1) & 1) * CK_STAGE, k0 + CK_TILE);
+      bad_cur = bad_next;
+      if (t + 2 < ntiles) fetch_slots(k0 + 2 * CK_TILE);
+    }
+    uint8_t* cur = lds + (t & 1) * CK_STAGE + wave * 32 * 256;  // this wave's 32 rows
+    const int k_valid = kend - (k0 + 32 * wave);
+    if (k_valid < 32 || bad_now != 0)
+      dense_tile<1, 32, true>(cur, cur + CK_TILE * 256, ad, qf, st, c, k_valid, bad_now);
+    else
+      dense_tile<1, 32, false>(cur, cur + CK_TILE * 256, ad, qf, st, c, 32);
+  }
+  __syncthreads();
+
+  // ---- merge the four wavefronts' states (each holds 32 M rows x its keys)
+  const float m_run = st.m_run[0];
+  const float l_tot = st.l_run[0] + __shfl_xor(st.l_run[0], 32);
+  float* red = reinterpret_cast<float*>(lds);
+  float* red_m = red;             // [4][32]
+  float* red_l = red + 4 * 32;    // [4][32]
+  float* ored = red + 8 * 32;     // [4][128][32]
+  if (hl == 0) {
+    red_m[wave * 32 + lrow] = m_run;
+    red_l[wave * 32 + lrow] = l_tot;
+  }
+  __syncthreads();
+  float m_all = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) m_all = fmaxf(m_all, red_m[w * 32 + lrow]);
+  const float m_all_use = (m_all == -INFINITY) ? 0.f : m_all;
+  const float fac = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run - m_all_use);
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int d = db * 32 + 8 * (i >> 2) + 4 * hl + (i & 3);
+      ored[(wave * HD + d) * 32 + lrow] = st.oacc[0][db][i] * fac;
+    }
+  __syncthreads();
+  const int q = tid >> 3;
+  const int d0 = (tid & 7) * 16;
+  float mq = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) mq = fmaxf(mq, red_m[w * 32 + q]);
+  const float mq_use = (mq == -INFINITY) ? 0.f : mq;
+  float lq = 0.f;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const float mw = red_m[w * 32 + q];
+    lq += (mw == -INFINITY) ? 0.f : red_l[w * 32 + q] * __builtin_amdgcn_exp2f(mw - mq_use);
+  }
+  float acc[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    float sum = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) sum += ored[(w * HD + d0 + i) * 32 + q];
+    acc[i] = sum;
+  }
+  const int mrow = m_base + q;
+  if (mrow < M) {
+    const int tq = mrow / g;
+    const int hq = hkv * g + (mrow - tq * g);
+    if (a.n_split == 1) {
+      const float inv = lq > 0.f ? 1.f / lq : 0.f;
+      uint16_t* op = a.o + (int64_t)(qrow0 + tq) * a.o_stride + hq * HD + d0;
+      u32x4_t w0, w1;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        w0[w] = cvt_pk_bf16(acc[2 * w] * inv, acc[2 * w + 1] * inv);
+        w1[w] = cvt_pk_bf16(acc[8 + 2 * w] * inv, acc[8 + 2 * w + 1] * inv);
+      }
+      st128(op, w0);
+      st128(op + 8, w1);
+    } else {
+      const int64_t Prec = (((int64_t)s * a.Hkv + hkv) * a.mtiles + mt) * a.n_split + split;
+      float* po = a.ws + (Prec * 32 + q) * HD + d0;
+#pragma unroll
+      for (int i = 0; i < 16; i += 4) {
+        f32x4_t v4 = {acc[i], acc[i + 1], acc[i + 2], acc[i + 3]};
+        *reinterpret_cast<f32x4_t*>(po + i) = v4;
+      }
+      if ((tid & 7) == 0) {
+        const int64_t nrec = (int64_t)a.n_seg * a.Hkv * a.mtiles * a.n_split;
+        float* pml = a.ws + nrec * 32 * HD + (Prec * 32 + q) * 2;
+        pml[0] = mq;
+        pml[1] = lq;
+      }
     }
   }
 }
@@ -907,8 +654,6 @@ static const float kLog2e = 1.4426950408889634f;
 // (256 M rows sharing each K/V tile) once a segment has >= 1024 M rows.
 constexpr int DENSE_ST = 2;
 constexpr int DENSE_LONG_M = 1024;
-// K3b: 1 x 32 M rows, 128-key tiles split over 4 wavefronts.
-using CachedCfg = Cfg<1, 4, 1>;
 
 static int common_checks(const char* name, const void* q, const void* k, const void* v, const void* o, int Hq,
                          int Hkv, int D, int64_t qs, int64_t ks, int64_t vs, int64_t os) {
@@ -983,8 +728,13 @@ extern "C" int dllm_attn_varlen_fwd(const dllm_bf16* q, const dllm_bf16* k, cons
   if (logical > (int64_t)1 << 30) return fail(DLLM_ERR_INVALID_ARG, "%s: problem too large", name);
   a.logical_blocks = (int)logical;
   a.scale_log2 = softmax_scale * kLog2e;
-  auto kern = wide ? attn_dense_kernel<8, 1, DENSE_ST> : attn_dense_kernel<4, 1, DENSE_ST>;
-  constexpr int lds_bytes = DENSE_ST * DK_STAGE_BYTES;
+#ifndef DENSE_SHORT_TK
+#define DENSE_SHORT_TK 64
+#define DENSE_SHORT_OCC 2
+#endif
+  auto kern = wide ? attn_dense_kernel<8, 1, DENSE_ST, 64, 2>
+                   : attn_dense_kernel<4, 1, DENSE_ST, DENSE_SHORT_TK, DENSE_SHORT_OCC>;
+  const int lds_bytes = DENSE_ST * 2 * (wide ? 64 : DENSE_SHORT_TK) * 256;
   if ((rc = set_lds(kern, lds_bytes, name))) return rc;
   const int nb = (int)((logical + 7) / 8 * 8);
   kern<<<dim3(nb), dim3(64 * nw), lds_bytes, reinterpret_cast<hipStream_t>(stream)>>>(a);
@@ -1002,10 +752,10 @@ static int block_cached_plan(int n_seg, int max_q, int max_keys, int Hq, int Hkv
   if (want > max_split) want = max_split;
   if (want < 1) want = 1;
   n_split = (int)want;
-  const int tiles = (max_keys + CachedCfg::NKT - 1) / CachedCfg::NKT;
+  const int tiles = (max_keys + CK_TILE - 1) / CK_TILE;
   const int tiles_per_split = (tiles + n_split - 1) / n_split;
-  keys_per_split = tiles_per_split * CachedCfg::NKT;
-  if (keys_per_split <= 0) keys_per_split = CachedCfg::NKT;
+  keys_per_split = tiles_per_split * CK_TILE;
+  if (keys_per_split <= 0) keys_per_split = CK_TILE;
   n_split = max_keys > 0 ? (max_keys + keys_per_split - 1) / keys_per_split : 1;
   return 0;
 }
@@ -1061,10 +811,10 @@ extern "C" int dllm_attn_block_cached_fwd(const dllm_bf16* q, const dllm_bf16* k
   a.logical_blocks = (int)logical;
   a.scale_log2 = softmax_scale * kLog2e;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  auto kern = attn_fwd_kernel<1, 4, 1, true>;
-  if ((rc = set_lds(kern, CachedCfg::LDS_BYTES, name))) return rc;
+  constexpr int lds_bytes = 2 * CK_STAGE;
+  if ((rc = set_lds(attn_cached_kernel, lds_bytes, name))) return rc;
   const int nb = (int)((logical + 7) / 8 * 8);
-  kern<<<dim3(nb), dim3(256), CachedCfg::LDS_BYTES, st>>>(a);
+  attn_cached_kernel<<<dim3(nb), dim3(256), lds_bytes, st>>>(a);
   if ((rc = check_launch(name))) return rc;
   if (n_split > 1) {
     const int64_t rows = (int64_t)n_seg * Hkv * mtiles * 32;

@@ -47,9 +47,12 @@ def varlen(q, k, v, cu_q, cu_k, scale: float, dtype=np.float64, seg_ids=None, ou
 
 
 def block_cached(q_blk, k_blk, v_blk, k_cache, v_cache, slots, scale: float, dtype=np.float64) -> np.ndarray:
-    """Mode 2: keys/values = [cache rows slots[0..n_c) ; block rows]."""
+    """Mode 2: keys/values = [cache rows slots[0..n_c) ; block rows].  Slots
+    outside the cache are left out (the kernels' documented rule; the
+    reference would read out of bounds)."""
     Hkv, D = k_blk.shape[1], k_blk.shape[2]
     slots = np.asarray(slots, dtype=np.int64)
+    slots = slots[(slots >= 0) & (slots < k_cache.shape[0])]
     kc = np.zeros((slots.size, Hkv, D), dtype=k_cache.dtype)
     vc = np.zeros((slots.size, Hkv, D), dtype=v_cache.dtype)
     _kv.load(kc, vc, k_cache, v_cache, slots)

@@ -150,3 +150,28 @@ def test_block_cached(dev, prefix, blk, Hq, Hkv):
         r0, r1 = cul[i], cul[i + 1]
         ref = oatt.block_cached(qn[r0:r1], kn[r0:r1], vn[r0:r1], kcn, vcn, slots[i], D ** -0.5, dtype=np.float32)
         assert_attn_close(o[r0:r1], ref, f"seq {i}")
+
+
+def test_block_cached_invalid_slots_are_excluded(dev):
+    """Slots outside the cache are left out of the softmax."""
+    print("block_cached invalid slots", flush=True)
+    q, k, v, cu, kc, vc, slots = _cached_case([300, 700], [32, 32], 8, 8, seed=77)
+    slots[0][5] = -3
+    slots[0][100] = kc.shape[0]
+    slots[1][699] = 10 ** 8
+    D = 128
+    off = [0, len(slots[0]), len(slots[0]) + len(slots[1])]
+    flat = torch.tensor(slots[0] + slots[1], dtype=torch.int32)
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    o = torch.zeros_like(qd)
+    ws_b = _capi.block_cached_workspace_size(2, 32, 732, 8, 8, D)
+    ws = torch.empty(max(ws_b, 1), dtype=torch.uint8, device=dev) if ws_b else None
+    _capi.attn_block_cached_fwd(qd, kd, vd, o, cu.to(dev), None, 2, 32, 732, kc.to(dev), vc.to(dev), flat.to(dev),
+                                torch.tensor(off, dtype=torch.int32, device=dev), D ** -0.5, ws)
+    torch.cuda.synchronize()
+    cul = cu.tolist()
+    for i in range(2):
+        r0, r1 = cul[i], cul[i + 1]
+        ref = oatt.block_cached(to_np(q)[r0:r1], to_np(k)[r0:r1], to_np(v)[r0:r1], to_np(kc), to_np(vc), slots[i],
+                                D ** -0.5, dtype=np.float32)
+        assert_attn_close(o[r0:r1], ref, f"seq {i}")

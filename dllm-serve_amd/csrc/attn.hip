@@ -80,6 +80,9 @@ __device__ __forceinline__ u32x4_t bload(__amdgpu_buffer_rsrc_t r, uint32_t voff
 // below 2^kLazy, well inside the bf16 / fp32 range.
 constexpr float kLazy = 8.0f;
 
+// Partial accumulators per S^T block (see dense_tile).
+constexpr int kSSplit = 2;
+
 // ---------------------------------------------------------------------------
 // K3a, dense varlen attention: K and V tiles go HBM -> LDS by buffer DMA
 // (buffer_load_dwordx4 ... lds, no VGPR staging); the V^T MFMA operand is
@@ -163,7 +166,7 @@ __device__ __forceinline__ void dense_softmax(f32x16_t (&sacc)[KB], f32x16_t (&o
       }
       mx = fmaxf(mx, sacc[b][i]);
     }
-  mx = fmaxf(mx, __shfl_xor(mx, 32)) * c;
+  mx = pair_max32(mx) * c;
   const bool need = mx > m_run + kLazy;
   if (__builtin_amdgcn_ballot_w64(need)) {
     const float m_new = need ? mx : m_run;
@@ -176,7 +179,9 @@ __device__ __forceinline__ void dense_softmax(f32x16_t (&sacc)[KB], f32x16_t (&o
     m_run = m_new;
   }
   const float neg_m = (m_run == -INFINITY) ? 0.f : -m_run;
-  float psum = 0.f;
+  // The row sum adds the bf16-rounded numerators, the same values the O^T
+  // product consumes; two partial sums keep the dependent chain short.
+  float psum[2] = {0.f, 0.f};
 #pragma unroll
   for (int b = 0; b < KB; ++b)
 #pragma unroll
@@ -186,12 +191,12 @@ __device__ __forceinline__ void dense_softmax(f32x16_t (&sacc)[KB], f32x16_t (&o
       for (int w = 0; w < 4; ++w) {
         const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[b][8 * j + 2 * w], c, neg_m));
         const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[b][8 * j + 2 * w + 1], c, neg_m));
-        psum += p0 + p1;
         pk[w] = cvt_pk_bf16(p0, p1);
+        psum[w & 1] = add_bf16x2(pk[w], psum[w & 1]);
       }
       pf[2 * b + j] = as_bf16x8(pk);
     }
-  l_run += psum;
+  l_run += psum[0] + psum[1];
 }
 
 // One 64-key tile for one wavefront owning NQ query blocks: every K and V^T
@@ -205,13 +210,20 @@ __device__ __forceinline__ void dense_tile(const uint8_t* Ks, const uint8_t* Vs,
   const int hl = lane >> 5;
   // kk outer, key block inner: the KB*NQ accumulators form independent MFMA
   // chains that interleave instead of one chain waiting on itself.
-  f32x16_t sacc[NQ][KB];
+  // Each S^T block's head-dim reduction is split over SPLIT partial
+  // accumulators (kk % SPLIT) so KB*NQ*SPLIT independent MFMA chains are in
+  // flight: a dependent 32x32x16 MFMA waits several issue slots for its
+  // predecessor, and two chains per wavefront leave the matrix pipe idle.
+  constexpr int SPLIT = kSSplit;
+  f32x16_t sp[NQ][KB][SPLIT];
 #pragma unroll
   for (int q = 0; q < NQ; ++q)
 #pragma unroll
     for (int b = 0; b < KB; ++b)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) sacc[q][b][i] = 0.f;
+      for (int h = 0; h < SPLIT; ++h)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) sp[q][b][h][i] = 0.f;
 #pragma unroll
   for (int kk = 0; kk < 8; ++kk) {
 #pragma unroll
@@ -220,9 +232,18 @@ __device__ __forceinline__ void dense_tile(const uint8_t* Ks, const uint8_t* Vs,
           as_bf16x8(*reinterpret_cast<const u32x4_t*>(Ks + b * 32 * 256 + (ad.kbase ^ (uint32_t)(32 * kk))));
 #pragma unroll
       for (int q = 0; q < NQ; ++q)
-        sacc[q][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, qf[q][kk], sacc[q][b], 0, 0, 0);
+        sp[q][b][kk % SPLIT] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, qf[q][kk], sp[q][b][kk % SPLIT], 0, 0, 0);
     }
   }
+  f32x16_t sacc[NQ][KB];
+#pragma unroll
+  for (int q = 0; q < NQ; ++q)
+#pragma unroll
+    for (int b = 0; b < KB; ++b) {
+      sacc[q][b] = sp[q][b][0];
+#pragma unroll
+      for (int h = 1; h < SPLIT; ++h) sacc[q][b] += sp[q][b][h];
+    }
   bf16x8_t pf[NQ][2 * KB];
 #pragma unroll
   for (int q = 0; q < NQ; ++q)
@@ -356,7 +377,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(OCC, OC
 
 #pragma unroll
   for (int q = 0; q < NQ; ++q) {
-    const float l_tot = st.l_run[q] + __shfl_xor(st.l_run[q], 32);
+    const float l_tot = pair_sum32(st.l_run[q]);
     if (okq[q]) {
       const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
       uint16_t* op = a.o + (int64_t)(qrow0 + tokq[q]) * a.o_stride + headq[q] * HD;
@@ -533,7 +554,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 
   // ---- merge the four wavefronts' states (each holds 32 M rows x its keys)
   const float m_run = st.m_run[0];
-  const float l_tot = st.l_run[0] + __shfl_xor(st.l_run[0], 32);
+  const float l_tot = pair_sum32(st.l_run[0]);
   float* red = reinterpret_cast<float*>(lds);
   float* red_m = red;             // [4][32]
   float* red_l = red + 4 * 32;    // [4][32]
@@ -728,13 +749,12 @@ extern "C" int dllm_attn_varlen_fwd(const dllm_bf16* q, const dllm_bf16* k, cons
   if (logical > (int64_t)1 << 30) return fail(DLLM_ERR_INVALID_ARG, "%s: problem too large", name);
   a.logical_blocks = (int)logical;
   a.scale_log2 = softmax_scale * kLog2e;
-#ifndef DENSE_SHORT_TK
-#define DENSE_SHORT_TK 64
-#define DENSE_SHORT_OCC 2
-#endif
-  auto kern = wide ? attn_dense_kernel<8, 1, DENSE_ST, 64, 2>
-                   : attn_dense_kernel<4, 1, DENSE_ST, DENSE_SHORT_TK, DENSE_SHORT_OCC>;
-  const int lds_bytes = DENSE_ST * 2 * (wide ? 64 : DENSE_SHORT_TK) * 256;
+  // Long segments: 8 wavefronts (256 M rows) per workgroup, 64-key tiles, two
+  // workgroups per CU.  Short ones: 4 wavefronts, 32-key tiles, three
+  // workgroups per CU (more resident wavefronts to overlap the softmax of one
+  // with the MFMAs of another; measured best at 8 x 384 and 8 x 512 tokens).
+  auto kern = wide ? attn_dense_kernel<8, 1, DENSE_ST, 64, 2> : attn_dense_kernel<4, 1, DENSE_ST, 32, 3>;
+  const int lds_bytes = DENSE_ST * 2 * (wide ? 64 : 32) * 256;
   if ((rc = set_lds(kern, lds_bytes, name))) return rc;
   const int nb = (int)((logical + 7) / 8 * 8);
   kern<<<dim3(nb), dim3(64 * nw), lds_bytes, reinterpret_cast<hipStream_t>(stream)>>>(a);

@@ -45,6 +45,27 @@ __device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi) {
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(u32x4_t v) { return __builtin_bit_cast(bf16x8_t, v); }
 
+// acc + lo + hi of a packed bf16 pair, exactly the values an MFMA B operand
+// holds (one v_dot2_f32_bf16 against (1, 1)).
+__device__ __forceinline__ float add_bf16x2(uint32_t pk, float acc) {
+  const bf16x2_t one = {(__bf16)1.0f, (__bf16)1.0f};
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pk), one, acc, false);
+}
+
+// Combine a value across the lane pair (l, l ^ 32) with v_permlane32_swap
+// (gfx950): after the swap one operand holds lanes 0..31 of x in both halves
+// and the other lanes 32..63.  Every lane of the wavefront must be active.
+__device__ __forceinline__ float pair_max32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x),
+                                                  false, false);
+  return fmaxf(__builtin_bit_cast(float, (uint32_t)r[0]), __builtin_bit_cast(float, (uint32_t)r[1]));
+}
+__device__ __forceinline__ float pair_sum32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x),
+                                                  false, false);
+  return __builtin_bit_cast(float, (uint32_t)r[0]) + __builtin_bit_cast(float, (uint32_t)r[1]);
+}
+
 // Non-temporal-free plain 128-bit global load / store.
 __device__ __forceinline__ u32x4_t ld128(const void* p) { return *reinterpret_cast<const u32x4_t*>(p); }
 __device__ __forceinline__ void st128(void* p, u32x4_t v) { *reinterpret_cast<u32x4_t*>(p) = v; }

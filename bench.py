@@ -254,11 +254,11 @@ class LLaDA8B:
         self.ln_f = torch.ones(H, device=dev, dtype=torch.bfloat16)
         self.attn = [Attention(cfg["heads"], cfg["head_dim"], cfg["head_dim"] ** -0.5, cfg["heads"], causal=False)
                      for _ in range(cfg["layers"])]
+        from dllm_serve_amd.layers.rotary_embedding import RotaryEmbedding
+
         D = cfg["head_dim"]
-        inv_freq = 1.0 / (cfg["theta"] ** (torch.arange(0, D, 2, dtype=torch.float32, device=dev) / D))
-        t = torch.arange(8192, dtype=torch.float32, device=dev)
-        f = torch.outer(t, inv_freq)
-        self.cos, self.sin = f.cos(), f.sin()
+        # q / k are column views of the QKV projection output: rotate in place (K7)
+        self.rope = RotaryEmbedding(D, D, 8192, cfg["theta"], inplace=True).to(dev)
 
     def bind_cache(self, num_pages):
         c = self.cfg
@@ -271,11 +271,6 @@ class LLaDA8B:
         xf = x.float()
         return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.cfg["eps"])).to(x.dtype) * w
 
-    def _rope(self, x, pos):
-        cos, sin = self.cos[pos].unsqueeze(1), self.sin[pos].unsqueeze(1)
-        x1, x2 = x.float().chunk(2, dim=-1)
-        return torch.cat((x1 * cos - x2 * sin, x2 * cos + x1 * sin), dim=-1).to(x.dtype)
-
     def forward(self, ids, pos):
         c = self.cfg
         H, nh, D = c["hidden"], c["heads"], c["head_dim"]
@@ -284,9 +279,8 @@ class LLaDA8B:
         for L, a in zip(self.layers, self.attn):
             x = self._rms(h, L["attn_norm"])
             qkv = x @ L["qkv"].t()
-            q = self._rope(qkv[:, :H].view(n, nh, D), pos)
-            k = self._rope(qkv[:, H:2 * H].view(n, nh, D), pos)
-            v = qkv[:, 2 * H:].view(n, nh, D)
+            q, k = self.rope(pos, qkv[:, :H], qkv[:, H:2 * H])
+            q, k, v = q.view(n, nh, D), k.view(n, nh, D), qkv[:, 2 * H:].view(n, nh, D)
             h = h + a(q, k, v) @ L["o"].t()
             x = self._rms(h, L["ff_norm"])
             gu = x @ L["gate_up"].t()
@@ -388,6 +382,33 @@ def bench_denoise_c4(dev):
     del model
     torch.cuda.empty_cache()
     return out
+
+
+def bench_rope(dev, n=8 * 384, Hq=32, Hkv=32, D=128, theta=500000.0):
+    """K7 at the C2 step's token count: q and k of one layer rotated in place
+    (positions of 8 sequences x 384), vs the reference's f32 tensor expression
+    evaluated by torch (rotary_embedding.py:6-17) on the same device."""
+    from dllm_serve_amd.layers.rotary_embedding import RotaryEmbedding
+
+    rope = RotaryEmbedding(D, D, 8192, theta, inplace=True).to(dev)
+    g = torch.Generator(device=dev).manual_seed(5)
+    qkv = torch.randn(n, (Hq + 2 * Hkv) * D, generator=g, device=dev, dtype=torch.bfloat16)
+    q, k = qkv[:, :Hq * D], qkv[:, Hq * D:(Hq + Hkv) * D]
+    pos = torch.arange(384, device=dev).repeat(n // 384)
+    ms = time_kernel(lambda: rope(pos, q, k), iters=100)
+    table = rope.cos_sin_cache
+
+    def torch_expr():
+        cs = table[pos]
+        cos, sin = cs[:, None, :D // 2], cs[:, None, D // 2:]
+        for x in (q.view(n, Hq, D), k.view(n, Hkv, D)):
+            x1, x2 = torch.chunk(x.to(torch.float32), 2, dim=-1)
+            torch.cat((x1 * cos - x2 * sin, x2 * cos + x1 * sin), dim=-1).to(x.dtype)
+
+    ms_torch = time_kernel(torch_expr, iters=20)
+    algo = 2.0 * 2 * n * (Hq + Hkv) * D + 4.0 * n * D  # q/k read + written, one table row per token
+    return dict(tokens=n, kernel_us=ms * 1e3, gbs=algo / (ms * 1e-3) / 1e9, frac_of_hbm=algo / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS,
+                torch_expr_us=ms_torch * 1e3, speedup_vs_torch_expr=ms_torch / ms)
 
 
 def cpu_baseline(lens, Hq, Hkv, D, budget_s=12.0):
@@ -497,6 +518,8 @@ def main() -> None:
         log("C5: block-cached attention + KV scatter")
         r5 = bench_block_cached(dev, args.quick)
         extra["c5_block_cached"] = {k: round(v, 3) for k, v in r5.items()}
+        log("K7: RoPE of q and k at the C2 step's token count")
+        extra["rope_c2_tokens"] = {k: round(v, 3) for k, v in bench_rope(dev).items()}
         log("C4: sparse vs dense attention per 64-step block")
         r4s = bench_sparse_c4(dev)
         extra["c4_head_sparse_per_block"] = {k: round(v, 3) for k, v in r4s.items()}

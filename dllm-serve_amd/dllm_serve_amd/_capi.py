@@ -51,6 +51,7 @@ SIGNATURES = {
         [_P, _P, _P, _I64, _I64, _I64, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _F,
          _P, _P, _I64, _P, _P, _P, _SZ, _P],
     ),
+    "dllm_rope_neox": (_I, [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _P, _I64, _I, _I, _I, _I, _P]),
 }
 
 _lib = None
@@ -181,3 +182,18 @@ def select_kv_store(q, k, v, jobs, n_job, max_kc, max_keep, max_blk, head_select
         k_cache.data_ptr(), v_cache.data_ptr(), k_cache.numel() // (Hkv * D),
         slots.data_ptr(), _ptr(idx_out), _ptr(workspace), ws_bytes, _stream(q.device))
     _check(rc, "dllm_select_kv_store")
+
+
+def rope_neox(q_in, q_out, k_in, k_out, positions, cos_sin_cache, n_tok, Hq, Hkv, D):
+    """K7: NeoX rotary embedding of q and k (token-major, last dim contiguous).
+    q_out / k_out may be q_in / k_in (in place)."""
+    _require_gpu(q_in, q_out, k_in, k_out, positions, cos_sin_cache)
+    lib = load()
+    rc = lib.dllm_rope_neox(
+        _ptr(q_in), q_in.stride(0) if q_in is not None else 0,
+        _ptr(q_out), q_out.stride(0) if q_out is not None else 0,
+        _ptr(k_in), k_in.stride(0) if k_in is not None else 0,
+        _ptr(k_out), k_out.stride(0) if k_out is not None else 0,
+        positions.data_ptr(), cos_sin_cache.data_ptr(), cos_sin_cache.shape[0],
+        n_tok, Hq, Hkv, D, _stream(positions.device))
+    _check(rc, "dllm_rope_neox")

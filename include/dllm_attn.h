@@ -163,6 +163,30 @@ int dllm_select_kv_store(const dllm_bf16* q, const dllm_bf16* k, const dllm_bf16
                          const int32_t* slots, int64_t* idx_out,
                          void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * K7 -- NeoX rotary embedding of q and k in one launch.  Replaces
+ * RotaryEmbedding.forward / apply_rotary_emb
+ * (dllmserve/layers/rotary_embedding.py:6-17,41-57), applied to q and k
+ * before attention at dllmserve/models/llada.py:81 and dream.py:90.
+ *
+ * cos_sin_cache is the reference's f32 table [max_position, D] (cos of the
+ * D/2 frequencies, then their sin; rotary_embedding.py:30-38).  For token i
+ * with p = positions[i] (int64), head h, j in [0, D/2):
+ *   x1 = x[i,h,j], x2 = x[i,h,j+D/2] as f32, c = table[p][j], s = table[p][D/2+j]
+ *   out[i,h,j]     = bf16(x1*c - x2*s)
+ *   out[i,h,j+D/2] = bf16(x2*c + x1*s)
+ * each product and sum rounded to f32 (no fused multiply-add), bf16 by
+ * round-to-nearest-even: bit-exact against that f32 expression evaluated op
+ * by op.  q is [n_tok, Hq, D] and k [n_tok, Hkv, D] with the given token
+ * strides; out may equal in (in place) but must not otherwise overlap it.
+ * A token whose position is outside [0, max_position) is not written (the
+ * reference's table lookup would fail).  D must be a multiple of 16.
+ */
+int dllm_rope_neox(const dllm_bf16* q_in, int64_t q_in_stride, dllm_bf16* q_out, int64_t q_out_stride,
+                   const dllm_bf16* k_in, int64_t k_in_stride, dllm_bf16* k_out, int64_t k_out_stride,
+                   const int64_t* positions, const float* cos_sin_cache, int64_t max_position,
+                   int n_tok, int Hq, int Hkv, int D, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

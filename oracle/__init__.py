@@ -13,7 +13,7 @@ Modules
   select     head / token KV selection with the explicit rounding and
              tie-break rule the GPU kernels implement
   kvcache    store_kvcache / load_kvcache by slot
-  rope       NeoX rotary embedding (input preparation)
+  rope       NeoX rotary embedding (input preparation; checker of the K7 kernel)
   configs    seeded synthetic inputs of the benchmark configurations
 
 Parity pins (what checks each function; see tests/test_oracle_*.py):
@@ -22,7 +22,9 @@ Parity pins (what checks each function; see tests/test_oracle_*.py):
   select     exact rational arithmetic + full sort on small inputs, torch.topk
              on tie-free inputs, torch bf16 einsum agreement, special cases
   kvcache    brute-force loops, round trips, untouched-slot sentinels
-  rope       norm preservation, relative-position invariance, position 0
+  rope       norm preservation, relative-position invariance, position 0,
+             quarter-turn / half-turn tables (exact swaps and negations),
+             agreement with the torch f32 expression
 The reference's own tests hold no numeric fixtures for this path, and its
 package cannot be imported here (it needs flash_attn), so no function is
 pinned against reference-produced vectors.

@@ -77,3 +77,31 @@ def test_missing_library_fails_loudly(tmp_path, monkeypatch):
     monkeypatch.setattr(_capi, "_lib", None)
     with pytest.raises(RuntimeError, match="no CPU fallback"):
         _capi.load(str(tmp_path / "absent.so"))
+
+
+def test_rope_validation_without_gpu():
+    lib = _capi.load()
+    P = ctypes.c_void_p
+    fake = P(4096)
+    rc, msg = _err(lib.dllm_rope_neox(fake, 512, fake, 512, fake, 512, fake, 512, fake, fake, 64,
+                                      4, 4, 4, 72, None))
+    assert rc == _capi.DLLM_ERR_UNSUPPORTED and "head_dim" in msg
+    rc, msg = _err(lib.dllm_rope_neox(P(4098), 512, fake, 512, fake, 512, fake, 512, fake, fake, 64,
+                                      4, 4, 4, 128, None))
+    assert rc == _capi.DLLM_ERR_INVALID_ARG and "aligned" in msg
+    rc, msg = _err(lib.dllm_rope_neox(fake, 100, fake, 512, fake, 512, fake, 512, fake, fake, 64,
+                                      4, 4, 4, 128, None))
+    assert rc == _capi.DLLM_ERR_INVALID_ARG and "stride" in msg
+    assert lib.dllm_rope_neox(fake, 512, fake, 512, fake, 512, fake, 512, fake, fake, 64, 0, 4, 4, 128, None) == 0
+
+
+def test_rope_module_refuses_cpu_tensors():
+    import torch
+    from dllm_serve_amd.layers.rotary_embedding import RotaryEmbedding, get_rope
+
+    assert get_rope(128, 128, 64, 10000.0) is get_rope(128, 128, 64, 10000.0)
+    rope = RotaryEmbedding(128, 128, 64, 10000.0)
+    assert rope.cos_sin_cache.shape == (64, 128) and rope.cos_sin_cache.dtype == torch.float32
+    q = torch.zeros(4, 2 * 128, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        rope(torch.arange(4), q, q.clone())

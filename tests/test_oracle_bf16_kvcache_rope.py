@@ -82,3 +82,53 @@ def test_rope_invariants_and_torch_agreement():
     # torch formulation used for the benchmark inputs agrees
     yt = configs.rope_torch(torch.from_numpy(x), torch.from_numpy(pos), 500000.0).numpy()
     assert np.abs(yt - y).max() < 1e-4
+
+
+def _bf16_values(rng, shape):
+    from oracle.bf16 import round_bf16
+    return round_bf16(rng.standard_normal(shape).astype(np.float32))
+
+
+def test_rope_table_turns_are_exact():
+    """Quarter turn (cos 0, sin 1) swaps the halves with a sign, half turn
+    negates, cos 1 / sin 0 is the identity -- exactly, so a transposed half, a
+    wrong sign or an interleaved (GPT-J) pairing fails."""
+    from oracle.bf16 import f32_to_bf16_bits
+    rng = np.random.default_rng(3)
+    N, H, D = 6, 2, 64
+    h = D // 2
+    x = _bf16_values(rng, (N, H, D))
+    table = np.zeros((3, D), np.float32)
+    table[0, :h] = 1.0                      # identity
+    table[1, h:] = 1.0                      # quarter turn
+    table[2, :h] = -1.0                     # half turn
+    pos = np.array([0, 1, 2, 1, 0, 2])
+    y = orope.rotate_table(x, pos, table)
+    for i, p in enumerate(pos):
+        if p == 0:
+            want = x[i]
+        elif p == 1:
+            want = np.concatenate([-x[i, :, h:], x[i, :, :h]], axis=-1)
+        else:
+            want = -x[i]
+        assert np.array_equal(y[i], f32_to_bf16_bits(want)), (i, p)
+
+
+def test_rope_table_matches_apply_and_torch_ops():
+    """With the f32 table of the module construction the table rotation equals
+    orope.apply rounded to bf16, and torch's f32 ops evaluated one by one."""
+    from oracle.bf16 import f32_to_bf16_bits
+    rng = np.random.default_rng(4)
+    N, H, D = 40, 3, 128
+    x = _bf16_values(rng, (N, H, D))
+    pos = rng.integers(0, 4096, N)
+    c, s = orope.cos_sin(np.arange(4096), D, 500000.0)
+    table = np.concatenate([c, s], axis=-1)
+    y = orope.rotate_table(x, pos, table)
+    assert np.array_equal(y, f32_to_bf16_bits(orope.apply(x, pos, 500000.0)))
+    xt = torch.from_numpy(x)
+    tt = torch.from_numpy(table)[torch.from_numpy(pos)]
+    ct, st = tt[:, None, :D // 2], tt[:, None, D // 2:]
+    x1, x2 = xt[..., :D // 2], xt[..., D // 2:]
+    yt = torch.cat((x1 * ct - x2 * st, x2 * ct + x1 * st), dim=-1).to(torch.bfloat16)
+    assert np.array_equal(y, yt.view(torch.int16).numpy().view(np.uint16))

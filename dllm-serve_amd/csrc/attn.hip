@@ -103,10 +103,14 @@ constexpr int kSSplit = 2;
 
 // s_waitcnt vmcnt(N), expcnt / lgkmcnt untouched (gfx9 encoding: vmcnt bits
 // [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8]).
+// The waitcnt intrinsic is not a memory operation for the compiler, so an
+// empty asm with a memory clobber follows it: no LDS read of the tile being
+// waited for can be hoisted above the wait.
 template <int N>
 __device__ __forceinline__ void vm_wait() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
+  asm volatile("" ::: "memory");
 }
 
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint8_t* lds_dst, uint32_t voff) {
@@ -201,7 +205,44 @@ __device__ __forceinline__ void dense_softmax(f32x16_t (&sacc)[KB], f32x16_t (&o
 
 // One 64-key tile for one wavefront owning NQ query blocks: every K and V^T
 // operand fragment read from LDS feeds NQ MFMAs.
-template <int NQ, int TK, bool MASK>
+// V^T operands of one 32-key block for callers whose tiles arrive by
+// global_load_lds: the compiler makes every transposing-read builtin wait for
+// all such DMA still in flight (it cannot tell the tiles apart), which would
+// drain the next tile's prefetch.  The 16 reads are one asm block that ends
+// with its own lgkmcnt(0) wait, so its outputs are complete when it returns.
+// Read (c, d, h) -- key chunk c, d block d, half h -- is at
+// vbase ^ 64 d + 4096 c + 2048 h; output index (4 c + d) * 2 + h.
+__device__ __forceinline__ void v_operands_untracked(const uint8_t* Vs, const DenseAddr& ad, u32x2_t (&r)[16]) {
+  uint32_t b[4];
+#pragma unroll
+  for (int d = 0; d < 4; ++d)
+    b[d] = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)(Vs + (ad.vbase ^ (uint32_t)(64 * d)));
+  asm volatile(
+      "ds_read_b64_tr_b16 %0, %16\n"
+      "ds_read_b64_tr_b16 %1, %16 offset:2048\n"
+      "ds_read_b64_tr_b16 %2, %17\n"
+      "ds_read_b64_tr_b16 %3, %17 offset:2048\n"
+      "ds_read_b64_tr_b16 %4, %18\n"
+      "ds_read_b64_tr_b16 %5, %18 offset:2048\n"
+      "ds_read_b64_tr_b16 %6, %19\n"
+      "ds_read_b64_tr_b16 %7, %19 offset:2048\n"
+      "ds_read_b64_tr_b16 %8, %16 offset:4096\n"
+      "ds_read_b64_tr_b16 %9, %16 offset:6144\n"
+      "ds_read_b64_tr_b16 %10, %17 offset:4096\n"
+      "ds_read_b64_tr_b16 %11, %17 offset:6144\n"
+      "ds_read_b64_tr_b16 %12, %18 offset:4096\n"
+      "ds_read_b64_tr_b16 %13, %18 offset:6144\n"
+      "ds_read_b64_tr_b16 %14, %19 offset:4096\n"
+      "ds_read_b64_tr_b16 %15, %19 offset:6144\n"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]), "=&v"(r[7]),
+        "=&v"(r[8]), "=&v"(r[9]), "=&v"(r[10]), "=&v"(r[11]), "=&v"(r[12]), "=&v"(r[13]), "=&v"(r[14]),
+        "=&v"(r[15])
+      : "v"(b[0]), "v"(b[1]), "v"(b[2]), "v"(b[3])
+      : "memory");
+}
+
+template <int NQ, int TK, bool MASK, bool UNTRACKED_V = false>
 __device__ __forceinline__ void dense_tile(const uint8_t* Ks, const uint8_t* Vs, const DenseAddr& ad,
                                            const bf16x8_t (&qf)[NQ][8], DenseState<NQ>& st, float c, int k_valid,
                                            uint64_t bad = 0) {
@@ -248,6 +289,22 @@ __device__ __forceinline__ void dense_tile(const uint8_t* Ks, const uint8_t* Vs,
 #pragma unroll
   for (int q = 0; q < NQ; ++q)
     dense_softmax<KB, MASK>(sacc[q], st.oacc[q], st.m_run[q], st.l_run[q], pf[q], c, k_valid, bad, hl);
+  if constexpr (UNTRACKED_V) {
+    static_assert(KB == 1, "one 32-key block per call");
+    u32x2_t r[16];
+    v_operands_untracked(Vs, ad, r);
+#pragma unroll
+    for (int cch = 0; cch < 2; ++cch)
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        const u32x2_t lo = r[(4 * cch + db) * 2], hi = r[(4 * cch + db) * 2 + 1];
+        const bf16x8_t af = as_bf16x8(u32x4_t{lo[0], lo[1], hi[0], hi[1]});
+#pragma unroll
+        for (int q = 0; q < NQ; ++q)
+          st.oacc[q][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, pf[q][cch], st.oacc[q][db], 0, 0, 0);
+      }
+    return;
+  }
   // key chunk outer, d block inner: 4*NQ independent accumulator chains.
 #pragma unroll
   for (int cch = 0; cch < 2 * KB; ++cch) {
@@ -446,23 +503,39 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   const uint32_t vchunk = (uint32_t)((P ^ (4 * rl)) * 16);
   const int64_t row_elems = (int64_t)a.Hkv * HD;
   const int32_t* sp = n_c > 0 ? a.slots + slot_base : a.slot_off;  // a valid dummy when there are none
-  int slot_next[8];
-  uint32_t bad_next = 0;  // wave-uniform mask of this wave's rows (bit 4j + rl) with an invalid slot
-  auto fetch_slots = [&](int k0) {
+  // Per-wave pipeline (a wavefront DMAs and reads only its own 32 rows of a
+  // tile, so no workgroup barrier is needed until the merge): the slots of
+  // tile t+2 are fetched before tile t+1's DMA is issued, so that after
+  // computing tile t the wave can issue tile t+2 into the stage it just
+  // freed while tile t+1 is still in flight -- two tiles in flight per wave.
+  // Vector memory operations complete in issue order, so each wait is "at
+  // most N newer operations outstanding": a tile is 16 DMA instructions, a
+  // slot fetch 8 loads.
+  // The slot loads are issued as inline asm so that the compiler's own wait
+  // insertion does not track them: it would otherwise wait for every
+  // outstanding load around the loop.  Each slot is read only after an
+  // explicit vm_wait that retires it and an empty asm that ties the value to
+  // that point (slots_ready).
+  auto fetch_slots = [&](int (&dst)[8], int k0) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int kidx = k0 + 32 * wave + 4 * j + rl;
-      slot_next[j] = sp[min(max(kidx, 0), max(n_c - 1, 0))];
+      const int32_t* src = sp + min(max(kidx, 0), max(n_c - 1, 0));
+      asm volatile("global_load_dword %0, %1, off" : "=v"(dst[j]) : "v"(src) : "memory");
     }
+  };
+  auto slots_ready = [&](int (&v)[8]) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) asm volatile("" : "+v"(v[j]));
   };
   // Rows past kend read the last valid row; a cached row with an invalid
   // slot reads block row 0 (never the cache, which may be absent).  Both are
   // masked out of the softmax, so only the address needs to be valid.
-  auto issue = [&](uint8_t* stage, int k0) {
+  auto issue = [&](uint8_t* stage, int k0, const int (&slot)[8]) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int kidx = min(k0 + 32 * wave + 4 * j + rl, max(kend - 1, 0));
-      const int64_t sl = slot_next[j];
+      const int64_t sl = slot[j];
       const bool cached = kidx < n_c;
       const bool ok = sl >= 0 && sl < a.cache_slots;
       const uint16_t* krow;
@@ -481,12 +554,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     }
   };
   // rows of this wave's block whose slot is invalid, as a 32-bit mask (bit = 4j + rl)
-  auto invalid_rows = [&](int k0) -> uint32_t {
+  auto invalid_rows = [&](int k0, const int (&slot)[8]) -> uint32_t {
     uint32_t m = 0;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int kidx = k0 + 32 * wave + 4 * j + rl;
-      const int64_t sl = slot_next[j];
+      const int64_t sl = slot[j];
       const bool bad = kidx < n_c && kidx < kend && (sl < 0 || sl >= a.cache_slots);
       const uint64_t b = __builtin_amdgcn_ballot_w64(bad);
       // lanes 16 rl' .. 16 rl' + 15 share row 4j + rl'
@@ -497,17 +570,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     return m;
   };
 
-  const int ntiles = (kend - kbeg + CK_TILE - 1) / CK_TILE;
-  uint32_t bad_cur = 0;
-  if (ntiles > 0) {
-    fetch_slots(kbeg);
-    bad_next = invalid_rows(kbeg);
-    issue(lds, kbeg);
-    bad_cur = bad_next;
-    if (ntiles > 1) fetch_slots(kbeg + CK_TILE);
-  }
-
-  // ---- Q^T fragments
+  // ---- Q^T fragments, loaded before the first slot fetch: the wait for
+  // those slots (in-order completion) retires them, so no wait on q remains
+  // inside the tile loop.
   const int m = m_base + lrow;
   const bool m_ok = m < M;
   const int tok = m_ok ? m / g : 0;
@@ -521,6 +586,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk) qf[0][kk] = as_bf16x8(bload(qrs, qoff + (uint32_t)kk * 32u, 0u));
   }
+  const int ntiles = (kend - kbeg + CK_TILE - 1) / CK_TILE;
+  int slot_ahead[8];          // slots of the next tile to issue
+  uint32_t bad_t0 = 0, bad_t1 = 0;  // invalid-row masks of tiles t and t+1
+  {
+    int cur[8];
+    fetch_slots(cur, kbeg);
+    vm_wait<0>();  // q and S(0); the compiler sees q retired on every path
+    slots_ready(cur);
+    if (ntiles > 0) {
+      bad_t0 = invalid_rows(kbeg, cur);
+      issue(lds, kbeg, cur);                                   // D(0)
+    }
+    if (ntiles > 1) {
+      fetch_slots(cur, kbeg + CK_TILE);
+      if (ntiles > 2) fetch_slots(slot_ahead, kbeg + 2 * CK_TILE);   // S(2) before D(1)
+      if (ntiles > 2)
+        vm_wait<8>();  // S(1) (and D(0)); S(2) may stay in flight
+      else
+        vm_wait<0>();
+      slots_ready(cur);
+      bad_t1 = invalid_rows(kbeg + CK_TILE, cur);
+      issue(lds + CK_STAGE, kbeg + CK_TILE, cur);              // D(1)
+    }
+  }
+
   DenseAddr ad;
   dense_addr(ad, lane, 0u, 0u);
   DenseState<1> st;
@@ -534,21 +624,35 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 
   for (int t = 0; t < ntiles; ++t) {
     const int k0 = kbeg + t * CK_TILE;
-    vm_wait<0>();      // this lane's DMA of tile t (and the slots of tile t+1) have landed
-    __syncthreads();   // everyone's DMA of tile t is visible; stage (t+1)&1 is free
-    uint32_t bad_now = bad_cur;
-    if (t + 1 < ntiles) {
-      bad_next = invalid_rows(k0 + CK_TILE);
-      issue(lds + ((t + 1) & 1) * CK_STAGE, k0 + CK_TILE);
-      bad_cur = bad_next;
-      if (t + 2 < ntiles) fetch_slots(k0 + 2 * CK_TILE);
-    }
+    // D(t) has landed once at most the operations issued after it -- S(t+2)
+    // and D(t+1), when they exist -- are outstanding.
+    if (t + 2 < ntiles)
+      vm_wait<24>();
+    else if (t + 1 < ntiles)
+      vm_wait<16>();
+    else
+      vm_wait<0>();
     uint8_t* cur = lds + (t & 1) * CK_STAGE + wave * 32 * 256;  // this wave's 32 rows
     const int k_valid = kend - (k0 + 32 * wave);
-    if (k_valid < 32 || bad_now != 0)
-      dense_tile<1, 32, true>(cur, cur + CK_TILE * 256, ad, qf, st, c, k_valid, bad_now);
+    if (k_valid < 32 || bad_t0 != 0)
+      dense_tile<1, 32, true, true>(cur, cur + CK_TILE * 256, ad, qf, st, c, k_valid, bad_t0);
     else
-      dense_tile<1, 32, false>(cur, cur + CK_TILE * 256, ad, qf, st, c, 32);
+      dense_tile<1, 32, false, true>(cur, cur + CK_TILE * 256, ad, qf, st, c, 32);
+    uint32_t bad_t2 = 0;
+    if (t + 2 < ntiles) {
+      // this wave's rows of stage t&1 are free again: issue D(t+2) there,
+      // after S(t+3) (slot_ahead holds S(t+2), landed behind D(t+1))
+      vm_wait<16>();  // S(t+2); D(t+1) may stay in flight
+      slots_ready(slot_ahead);
+      int cur_slots[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) cur_slots[j] = slot_ahead[j];
+      if (t + 3 < ntiles) fetch_slots(slot_ahead, k0 + 3 * CK_TILE);
+      bad_t2 = invalid_rows(k0 + 2 * CK_TILE, cur_slots);
+      issue(lds + (t & 1) * CK_STAGE, k0 + 2 * CK_TILE, cur_slots);
+    }
+    bad_t0 = bad_t1;
+    bad_t1 = bad_t2;
   }
   __syncthreads();
 

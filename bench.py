@@ -129,9 +129,11 @@ def bench_dense(lens, Hq, Hkv, D, n_layers, steps, warmup, dev, seed=0):
                 kernel_us=ms_kernel * 1e3, tflops_kernel=flops_call / (ms_kernel * 1e-3) / 1e12)
 
 
-def bench_block_cached(dev, quick):
-    """C5: 32 x 32-token blocks against 2-4k-token cached prefixes in shuffled
-    256-row pages (LLaDA shape); the prefix is written with store_kvcache."""
+def c5_case(dev):
+    """C5 inputs resident on the device: 32 x 32-token blocks against 2-4k-token
+    cached prefixes in shuffled 256-row pages (LLaDA shape).  Returns the two
+    launches -- store_kvcache of the prefixes and the block-cached attention --
+    and their algorithmic bytes / FLOPs."""
     from oracle import configs
     from dllm_serve_amd import _capi
     from dllm_serve_amd.layers.attention import store_kvcache
@@ -145,9 +147,6 @@ def bench_block_cached(dev, quick):
     slots = torch.tensor([x for s in c["slots"] for x in s], dtype=torch.int32, device=dev)
     k_pre, v_pre = c["k_pre"].to(dev), c["v_pre"].to(dev)
     n_pre = k_pre.shape[0]
-    ms_store = time_kernel(lambda: store_kvcache(k_pre, v_pre, kc.view(-1, page, Hkv, D),
-                                                 vc.view(-1, page, Hkv, D), slots), iters=20)
-    store_bytes = 8.0 * n_pre * Hkv * D + 4.0 * n_pre
     q, k, v = c["q"].to(dev), c["k"].to(dev), c["v"].to(dev)
     B, blk = len(c["prefix"]), c["blk"]
     cu = torch.arange(0, (B + 1) * blk, blk, dtype=torch.int32, device=dev)
@@ -159,12 +158,38 @@ def bench_block_cached(dev, quick):
     ws_b = _capi.block_cached_workspace_size(B, blk, max_keys, Hq, Hkv, D)
     ws = torch.empty(max(ws_b, 1), dtype=torch.uint8, device=dev)
     o = torch.empty_like(q)
-    ms = time_kernel(lambda: _capi.attn_block_cached_fwd(q, k, v, o, cu, None, B, blk, max_keys, kc, vc, slots,
-                                                         slot_off, D ** -0.5, ws if ws_b else None), iters=50)
-    flops = sum(4.0 * blk * (p + blk) * Hq * D for p in c["prefix"])
-    byts = sum(2.0 * (2 * blk * Hq * D + 2 * (p + blk) * Hkv * D) + 4.0 * p for p in c["prefix"])
-    return dict(kernel_us=ms * 1e3, gbs=byts / (ms * 1e-3) / 1e9, tflops=flops / (ms * 1e-3) / 1e12,
-                bytes_per_call=byts, store_us=ms_store * 1e3, store_gbs=store_bytes / (ms_store * 1e-3) / 1e9)
+
+    def store():
+        store_kvcache(k_pre, v_pre, kc.view(-1, page, Hkv, D), vc.view(-1, page, Hkv, D), slots)
+
+    def attend():
+        _capi.attn_block_cached_fwd(q, k, v, o, cu, None, B, blk, max_keys, kc, vc, slots, slot_off, D ** -0.5,
+                                    ws if ws_b else None)
+
+    return dict(store=store, attend=attend, store_bytes=8.0 * n_pre * Hkv * D + 4.0 * n_pre,
+                flops=sum(4.0 * blk * (p + blk) * Hq * D for p in c["prefix"]),
+                bytes=sum(2.0 * (2 * blk * Hq * D + 2 * (p + blk) * Hkv * D) + 4.0 * p for p in c["prefix"]))
+
+
+def bench_block_cached(dev, quick):
+    """C5 timing: the KV scatter of the prefixes, then the block-cached attention."""
+    c = c5_case(dev)
+    ms_store = time_kernel(c["store"], iters=20)
+    ms = time_kernel(c["attend"], iters=50)
+    byts = c["bytes"]
+    return dict(kernel_us=ms * 1e3, gbs=byts / (ms * 1e-3) / 1e9, tflops=c["flops"] / (ms * 1e-3) / 1e12,
+                bytes_per_call=byts, store_us=ms_store * 1e3, store_gbs=c["store_bytes"] / (ms_store * 1e-3) / 1e9)
+
+
+def bench_copy(dev, nbytes=1 << 30):
+    """A plain device-to-device copy of 1 GiB (torch / HIP runtime): the
+    practical HBM rate the copy-like kernels (KV scatter, RoPE, block-cached
+    reads) are compared with."""
+    src = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    ms = time_kernel(lambda: dst.copy_(src), iters=10, warmup=2)
+    del src, dst
+    return dict(bytes=2.0 * nbytes, us=ms * 1e3, gbs=2.0 * nbytes / (ms * 1e-3) / 1e9)
 
 
 def bench_sparse_c4(dev, steps_block=64, quick=False):
@@ -451,7 +476,21 @@ def profile_run(lens, Hq, Hkv, D, n_layers, dev):
         o = torch.empty_like(q)
         _capi.attn_varlen_fwd(q, k, v, o, cu, cu, None, len(lens), max(lens), D ** -0.5)
     torch.cuda.synchronize()
-    log(f"profile run done: 3 x 256 MiB copies, {n_layers} attention launches")
+    # RoPE of one layer's q and k at the same token count, in place
+    from dllm_serve_amd.layers.rotary_embedding import RotaryEmbedding
+    rope = RotaryEmbedding(D, D, 8192, 500000.0, inplace=True).to(dev)
+    n = int(sum(lens))
+    pos = torch.cat([torch.arange(x, device=dev) for x in lens])
+    for q, k, _ in layers:
+        rope(pos, q, k)
+    # C5: the prefix scatter once, then four block-cached attention launches
+    c5 = c5_case(dev)
+    c5["store"]()
+    for _ in range(4):
+        c5["attend"]()
+    torch.cuda.synchronize()
+    log(f"profile run done: 3 x 256 MiB copies, {n_layers} attention launches, {n_layers} RoPE launches "
+        f"({n} tokens), 1 C5 store + 4 C5 block-cached launches")
 
 
 TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "attn_dense_kernel_llada_c2_8x384_counters.md")
@@ -479,8 +518,9 @@ def main() -> None:
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--quick", action="store_true", help="headline only (no extra shapes, no CPU baseline)")
     ap.add_argument("--profile", action="store_true",
-                    help="counter run: a 256 MiB device copy (x3, calibrates FETCH_SIZE / WRITE_SIZE) then 32 "
-                         "launches of the headline attention kernel; prints no JSON")
+                    help="counter run: a 256 MiB device copy (x3, calibrates FETCH_SIZE / WRITE_SIZE), 32 "
+                         "launches of the headline attention kernel, 32 RoPE launches, the C5 store and 4 C5 "
+                         "block-cached launches; prints no JSON")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); this build has no multi-GPU path",
@@ -518,6 +558,8 @@ def main() -> None:
         log("C5: block-cached attention + KV scatter")
         r5 = bench_block_cached(dev, args.quick)
         extra["c5_block_cached"] = {k: round(v, 3) for k, v in r5.items()}
+        log("HBM: plain 1 GiB device copy")
+        extra["hbm_copy_1gib"] = {k: round(v, 1) for k, v in bench_copy(dev).items()}
         log("K7: RoPE of q and k at the C2 step's token count")
         extra["rope_c2_tokens"] = {k: round(v, 3) for k, v in bench_rope(dev).items()}
         log("C4: sparse vs dense attention per 64-step block")

@@ -531,26 +531,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   // Rows past kend read the last valid row; a cached row with an invalid
   // slot reads block row 0 (never the cache, which may be absent).  Both are
   // masked out of the softmax, so only the address needs to be valid.
+  // Row addresses, branch-free: a row comes from the cache (base + slot *
+  // cache row bytes) or from the block (base + block row * token stride);
+  // each is one 32 x 32 -> 64-bit multiply-add.  Slots are int32, so one
+  // unsigned compare against the slot count also rejects negative slots.
+  const uint32_t cache_row_b = (uint32_t)(row_elems * 2);
+  const uint32_t n_slots = (uint32_t)min(a.cache_slots, (int64_t)1 << 31);
+  const uint32_t kS_b = (uint32_t)(a.k_stride * 2), vS_b = (uint32_t)(a.v_stride * 2);
+  const uint64_t kc0 = (uint64_t)(uintptr_t)(a.k_cache + hkv * HD);
+  const uint64_t vc0 = (uint64_t)(uintptr_t)(a.v_cache + hkv * HD);
+  const uint64_t kb0 = (uint64_t)(uintptr_t)(a.k + (int64_t)qrow0 * a.k_stride + hkv * HD);
+  const uint64_t vb0 = (uint64_t)(uintptr_t)(a.v + (int64_t)qrow0 * a.v_stride + hkv * HD);
   auto issue = [&](uint8_t* stage, int k0, const int (&slot)[8]) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int kidx = min(k0 + 32 * wave + 4 * j + rl, max(kend - 1, 0));
-      const int64_t sl = slot[j];
+      const uint32_t sl = (uint32_t)slot[j];
       const bool cached = kidx < n_c;
-      const bool ok = sl >= 0 && sl < a.cache_slots;
-      const uint16_t* krow;
-      const uint16_t* vrow;
-      if (cached && ok) {
-        krow = a.k_cache + sl * row_elems + hkv * HD;
-        vrow = a.v_cache + sl * row_elems + hkv * HD;
-      } else {
-        const int64_t br = qrow0 + (cached ? 0 : kidx - n_c);
-        krow = a.k + br * a.k_stride + hkv * HD;
-        vrow = a.v + br * a.v_stride + hkv * HD;
-      }
+      const bool use_cache = cached && sl < n_slots;
+      // a cached row with an invalid slot reads block row 0 (masked later)
+      const uint32_t idx = use_cache ? sl : (cached ? 0u : (uint32_t)(kidx - n_c));
+      const uint64_t kaddr = (use_cache ? kc0 : kb0) + (uint64_t)idx * (use_cache ? cache_row_b : kS_b);
+      const uint64_t vaddr = (use_cache ? vc0 : vb0) + (uint64_t)idx * (use_cache ? cache_row_b : vS_b);
       const int q = 8 * wave + j;
-      gdma16(reinterpret_cast<const uint8_t*>(krow) + (kchunk ^ (uint32_t)(64 * (j & 3))), stage + q * 1024);
-      gdma16(reinterpret_cast<const uint8_t*>(vrow) + vchunk, stage + CK_TILE * 256 + q * 1024);
+      gdma16(reinterpret_cast<const uint8_t*>(kaddr) + (kchunk ^ (uint32_t)(64 * (j & 3))), stage + q * 1024);
+      gdma16(reinterpret_cast<const uint8_t*>(vaddr) + vchunk, stage + CK_TILE * 256 + q * 1024);
     }
   };
   // rows of this wave's block whose slot is invalid, as a 32-bit mask (bit = 4j + rl)
@@ -559,8 +564,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int kidx = k0 + 32 * wave + 4 * j + rl;
-      const int64_t sl = slot[j];
-      const bool bad = kidx < n_c && kidx < kend && (sl < 0 || sl >= a.cache_slots);
+      const bool bad = kidx < n_c && kidx < kend && (uint32_t)slot[j] >= n_slots;
       const uint64_t b = __builtin_amdgcn_ballot_w64(bad);
       // lanes 16 rl' .. 16 rl' + 15 share row 4j + rl'
 #pragma unroll
@@ -909,6 +913,8 @@ extern "C" int dllm_attn_block_cached_fwd(const dllm_bf16* q, const dllm_bf16* k
   if (!cu || !slot_off) return fail(DLLM_ERR_INVALID_ARG, "%s: null cu / slot_off", name);
   if ((int64_t)max_q * q_stride_tok * 2 + 4096 >= ((int64_t)1 << 32))
     return fail(DLLM_ERR_UNSUPPORTED, "%s: a block spans more than 4 GiB of q", name);
+  if (k_stride_tok * 2 >= ((int64_t)1 << 32) || v_stride_tok * 2 >= ((int64_t)1 << 32))
+    return fail(DLLM_ERR_UNSUPPORTED, "%s: k / v token strides must be below 4 GiB", name);
   if (cache_slots > 0 && (!k_cache || !v_cache || !slots))
     return fail(DLLM_ERR_INVALID_ARG, "%s: null cache / slots", name);
   if (cache_slots > 0 && (!aligned16(k_cache) || !aligned16(v_cache)))

@@ -425,10 +425,20 @@ def bench_rope(dev, n=8 * 384, Hq=32, Hkv=32, D=128, theta=500000.0):
 
     rope = RotaryEmbedding(D, D, 8192, theta, inplace=True).to(dev)
     g = torch.Generator(device=dev).manual_seed(5)
-    qkv = torch.randn(n, (Hq + 2 * Hkv) * D, generator=g, device=dev, dtype=torch.bfloat16)
-    q, k = qkv[:, :Hq * D], qkv[:, Hq * D:(Hq + Hkv) * D]
+    # eight layers' QKV outputs (600 MB, beyond the 256 MB last-level cache),
+    # rotated in turn, so the timing reads and writes HBM
+    bufs = [torch.randn(n, (Hq + 2 * Hkv) * D, generator=g, device=dev, dtype=torch.bfloat16) for _ in range(8)]
+    views = [(b[:, :Hq * D], b[:, Hq * D:(Hq + Hkv) * D]) for b in bufs]
     pos = torch.arange(384, device=dev).repeat(n // 384)
-    ms = time_kernel(lambda: rope(pos, q, k), iters=100)
+    state = {"i": 0}
+
+    def one():
+        q_, k_ = views[state["i"] % len(views)]
+        state["i"] += 1
+        rope(pos, q_, k_)
+
+    ms = time_kernel(one, iters=96)
+    q, k = views[0]
     table = rope.cos_sin_cache
 
     def torch_expr():
@@ -439,6 +449,7 @@ def bench_rope(dev, n=8 * 384, Hq=32, Hkv=32, D=128, theta=500000.0):
             torch.cat((x1 * cos - x2 * sin, x2 * cos + x1 * sin), dim=-1).to(x.dtype)
 
     ms_torch = time_kernel(torch_expr, iters=20)
+    del bufs, views
     algo = 2.0 * 2 * n * (Hq + Hkv) * D + 4.0 * n * D  # q/k read + written, one table row per token
     return dict(tokens=n, kernel_us=ms * 1e3, gbs=algo / (ms * 1e-3) / 1e9, frac_of_hbm=algo / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS,
                 torch_expr_us=ms_torch * 1e3, speedup_vs_torch_expr=ms_torch / ms)

@@ -462,8 +462,12 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(OCC, OC
 constexpr int CK_TILE = 128;
 constexpr int CK_STAGE = 2 * CK_TILE * 256;
 
+// Cache and block rows of a segment are read by exactly one workgroup, each
+// 16-byte piece by one lane of one DMA instruction: streaming loads (the q
+// loads keep the default policy: a lane reads each q line in four 32-byte
+// steps and relies on the cache between them).
 __device__ __forceinline__ void gdma16(const void* g, uint8_t* lds_dst) {
-  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds_dst, 16, 0, 0);
+  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds_dst, 16, 0, kStreamAux);
 }
 
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void attn_cached_kernel(AttnArgs a) {

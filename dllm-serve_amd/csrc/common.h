@@ -66,8 +66,16 @@ __device__ __forceinline__ float pair_sum32(float x) {
   return __builtin_bit_cast(float, (uint32_t)r[0]) + __builtin_bit_cast(float, (uint32_t)r[1]);
 }
 
-// Non-temporal-free plain 128-bit global load / store.
+// Plain 128-bit global load / store.
 __device__ __forceinline__ u32x4_t ld128(const void* p) { return *reinterpret_cast<const u32x4_t*>(p); }
+
+// Cache-policy bits of the load builtins: 2 = nt (streaming: the line is
+// read once and need not stay in L2 ahead of reused data).
+constexpr int kStreamAux = 2;
+// 128-bit load of data read exactly once, with the nt hint.
+__device__ __forceinline__ u32x4_t ld128_stream(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+}
 __device__ __forceinline__ void st128(void* p, u32x4_t v) { *reinterpret_cast<u32x4_t*>(p) = v; }
 
 }  // namespace dllm

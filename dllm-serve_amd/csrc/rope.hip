@@ -61,8 +61,8 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
     src = a.k_in + (int64_t)i * a.ki_stride + (h - a.Hq) * a.D;
     dst = a.k_out + (int64_t)i * a.ko_stride + (h - a.Hq) * a.D;
   }
-  const u32x4_t x1 = ld128(src + 8 * c);
-  const u32x4_t x2 = ld128(src + half + 8 * c);
+  const u32x4_t x1 = ld128_stream(src + 8 * c);
+  const u32x4_t x2 = ld128_stream(src + half + 8 * c);
   const float* row = a.cos_sin + p * a.D;
   const f32x4_t c0 = *reinterpret_cast<const f32x4_t*>(row + 8 * c);
   const f32x4_t c1 = *reinterpret_cast<const f32x4_t*>(row + 8 * c + 4);

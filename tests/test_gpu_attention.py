@@ -55,6 +55,37 @@ def test_varlen_ragged(dev, lens, Hq, Hkv):
     assert_attn_close(o, ref, f"lens={lens}")
 
 
+@pytest.mark.parametrize("lens,Hq,Hkv", [
+    ([2100, 300, 2048], 16, 16),      # >= 2048 keys: 8-wavefront launch, ragged last tile
+    ([2500, 37], 28, 4),              # Dream GQA on the 8-wavefront launch
+])
+def test_varlen_long_key_streams(dev, lens, Hq, Hkv):
+    print(f"varlen long lens={lens} Hq={Hq} Hkv={Hkv}", flush=True)
+    q, k, v, cu = configs.packed_qkv(lens, Hq, Hkv, 128, seed=sum(lens) + Hq)
+    o = _run_varlen(q, k, v, cu, dev)
+    ref = oatt.varlen(to_np(q), to_np(k), to_np(v), cu.numpy(), cu.numpy(), 128 ** -0.5, dtype=np.float32)
+    assert_attn_close(o, ref, f"lens={lens}")
+
+
+@pytest.mark.parametrize("lq,lk", [([40, 7, 300], [100, 2200, 5]), ([128, 64], [64, 128])])
+def test_varlen_different_q_and_k_lengths(dev, lq, lk):
+    """cu_seqlens_q != cu_seqlens_k, as flash_attn_varlen_func allows."""
+    print(f"varlen lq={lq} lk={lk}", flush=True)
+    H, D = 8, 128
+    g = torch.Generator().manual_seed(sum(lq) + sum(lk))
+    q = torch.randn(sum(lq), H, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(sum(lk), H, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(sum(lk), H, D, generator=g).to(torch.bfloat16)
+    cu_q = torch.tensor([0] + list(np.cumsum(lq)), dtype=torch.int32)
+    cu_k = torch.tensor([0] + list(np.cumsum(lk)), dtype=torch.int32)
+    o = torch.zeros(sum(lq), H, D, dtype=torch.bfloat16, device=dev)
+    _capi.attn_varlen_fwd(q.to(dev), k.to(dev), v.to(dev), o, cu_q.to(dev), cu_k.to(dev), None, len(lq), max(lq),
+                          D ** -0.5, max_seqlen_k=max(lk))
+    torch.cuda.synchronize()
+    ref = oatt.varlen(to_np(q), to_np(k), to_np(v), cu_q.numpy(), cu_k.numpy(), D ** -0.5, dtype=np.float32)
+    assert_attn_close(o, ref, f"lq={lq} lk={lk}")
+
+
 def test_varlen_subset_leaves_other_rows(dev):
     """seg_ids runs only some segments in place; other rows keep their contents."""
     print("varlen seg_ids subset", flush=True)

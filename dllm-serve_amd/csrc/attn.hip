@@ -432,22 +432,58 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(OCC, OC
     dense_tile<NQ, TK, true>(cur, cur + TK * 256, ad, qf, st, c, Lk - t * TK);
   }
 
+  if constexpr (NQ == 1) {
+    // O goes through LDS so that every global store writes whole 256-byte
+    // rows: lane (lrow, hl) holds, per d block db and quad rq, d = 32 db +
+    // 8 rq + 4 hl + 0..3, i.e. half hl of 16-byte chunk 4 db + rq of its row.
+    // The wave's 32 rows x 256 bytes land in its own 8 KiB of the (now free)
+    // K/V stages, chunks XOR-swizzled by row; read back, instruction j
+    // carries rows 4j .. 4j+3, one 16-byte chunk per lane.
+    static_assert(NW * 8192 <= ST * STAGE, "O staging fits in the K/V stages");
+    const float l_tot = pair_sum32(st.l_run[0]);
+    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    __syncthreads();  // every wavefront is done reading the K/V stages
+    uint8_t* ot = lds + wave * 8192;
 #pragma unroll
-  for (int q = 0; q < NQ; ++q) {
-    const float l_tot = pair_sum32(st.l_run[q]);
-    if (okq[q]) {
-      const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-      uint16_t* op = a.o + (int64_t)(qrow0 + tokq[q]) * a.o_stride + headq[q] * HD;
+    for (int db = 0; db < 4; ++db)
 #pragma unroll
-      for (int db = 0; db < 4; ++db)
+      for (int rq = 0; rq < 4; ++rq) {
+        u32x2_t w;
+        w[0] = cvt_pk_bf16(st.oacc[0][db][4 * rq + 0] * inv, st.oacc[0][db][4 * rq + 1] * inv);
+        w[1] = cvt_pk_bf16(st.oacc[0][db][4 * rq + 2] * inv, st.oacc[0][db][4 * rq + 3] * inv);
+        const int chunk = 4 * db + rq;
+        *reinterpret_cast<u32x2_t*>(ot + lrow * 256 + ((chunk ^ (lrow & 15)) * 16) + 8 * hl) = w;
+      }
+    const int rsub = lane >> 4, ch = lane & 15;
 #pragma unroll
-        for (int rq = 0; rq < 4; ++rq) {
-          const int d = db * 32 + 8 * rq + 4 * hl;
-          u32x2_t w;
-          w[0] = cvt_pk_bf16(st.oacc[q][db][4 * rq + 0] * inv, st.oacc[q][db][4 * rq + 1] * inv);
-          w[1] = cvt_pk_bf16(st.oacc[q][db][4 * rq + 2] * inv, st.oacc[q][db][4 * rq + 3] * inv);
-          *reinterpret_cast<u32x2_t*>(op + d) = w;
-        }
+    for (int j = 0; j < 8; ++j) {
+      const int r = 4 * j + rsub;
+      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(ot + r * 256 + ((ch ^ (r & 15)) * 16));
+      const int m = m_base + wave * 32 + r;
+      if (m < M) {
+        const int tok = m / g;
+        const int head = hkv * g + (m - tok * g);
+        st128(a.o + (int64_t)(qrow0 + tok) * a.o_stride + head * HD + ch * 8, v);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const float l_tot = pair_sum32(st.l_run[q]);
+      if (okq[q]) {
+        const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+        uint16_t* op = a.o + (int64_t)(qrow0 + tokq[q]) * a.o_stride + headq[q] * HD;
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+          for (int rq = 0; rq < 4; ++rq) {
+            const int d = db * 32 + 8 * rq + 4 * hl;
+            u32x2_t w;
+            w[0] = cvt_pk_bf16(st.oacc[q][db][4 * rq + 0] * inv, st.oacc[q][db][4 * rq + 1] * inv);
+            w[1] = cvt_pk_bf16(st.oacc[q][db][4 * rq + 2] * inv, st.oacc[q][db][4 * rq + 3] * inv);
+            *reinterpret_cast<u32x2_t*>(op + d) = w;
+          }
+      }
     }
   }
 }

@@ -32,7 +32,6 @@
 namespace dllm {
 
 constexpr int HD = 128;       // head dim handled by this build
-constexpr int KSTR = HD + 8;  // LDS row stride (elements) of the K tile: 272 B, conflict-free 16 B reads
 
 struct AttnArgs {
   const uint16_t* q;
@@ -203,8 +202,8 @@ __device__ __forceinline__ void dense_softmax(f32x16_t (&sacc)[KB], f32x16_t (&o
   l_run += psum[0] + psum[1];
 }
 
-// One 64-key tile for one wavefront owning NQ query blocks: every K and V^T
-// operand fragment read from LDS feeds NQ MFMAs.
+// One key tile (TK keys) for one wavefront owning NQ query blocks: every K
+// and V^T operand fragment read from LDS feeds NQ MFMAs.
 // V^T operands of one 32-key block for callers whose tiles arrive by
 // global_load_lds: the compiler makes every transposing-read builtin wait for
 // all such DMA still in flight (it cannot tell the tiles apart), which would
@@ -489,12 +488,13 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(OCC, OC
 }
 
 // ---------------------------------------------------------------------------
-// K3b v2: block rows vs [cached rows (by slot) ; block rows], same DMA + swizzled
-// LDS tiles as K3a.  Tile = 128 keys; wavefront w DMAs tile rows 32w..32w+31
-// (8 K + 8 V instructions, per-lane 64-bit addresses so caches above 4 GiB work)
-// and computes exactly those 32 keys for the workgroup's 32 M rows; the four
-// wavefronts' softmax states are merged in LDS at the end.  A cached row whose
-// slot is outside the cache is excluded (masked) from the softmax.
+// K3b: block rows vs [cached rows (by slot) ; block rows], with the swizzled
+// LDS tile layout of K3a.  Tile = 128 keys; wavefront w DMAs tile rows
+// 32w..32w+31 (8 K + 8 V instructions, per-lane 64-bit addresses so caches
+// above 4 GiB work) and computes exactly those 32 keys for the workgroup's 32
+// M rows; the four wavefronts' softmax states are merged in LDS at the end.
+// A cached row whose slot is outside the cache is excluded (masked) from the
+// softmax.
 constexpr int CK_TILE = 128;
 constexpr int CK_STAGE = 2 * CK_TILE * 256;
 

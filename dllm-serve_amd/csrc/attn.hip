@@ -917,8 +917,11 @@ static int block_cached_plan(int n_seg, int max_q, int max_keys, int Hq, int Hkv
   const int g = Hq / Hkv;
   mtiles = (max_q * g + 31) / 32;
   const int64_t pairs = (int64_t)n_seg * Hkv * mtiles;
-  // Aim for >= 2 workgroups per CU (256 CUs) with at least two 128-key tiles per split.
-  int64_t want = pairs > 0 ? (512 + pairs - 1) / pairs : 1;
+  // Aim for one workgroup per CU (256 CUs; the kernel's 128 KiB of LDS allow
+  // only one) with at least two 128-key tiles per split.  More splits would
+  // run as a second generation of workgroups plus the combine launch: 8 x 32
+  // rows against 288 cached rows took 36 us with 512 workgroups, 17 us with 256.
+  int64_t want = pairs > 0 ? (256 + pairs - 1) / pairs : 1;
   const int max_split = max_keys > 0 ? (max_keys + 255) / 256 : 1;
   if (want > max_split) want = max_split;
   if (want < 1) want = 1;

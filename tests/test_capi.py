@@ -36,7 +36,7 @@ def test_library_exports_every_declared_symbol():
 def test_workspace_size_functions():
     # one split: no workspace; few long segments: split over keys
     assert _capi.block_cached_workspace_size(1024, 32, 4000, 32, 32, 128) == 0
-    ws = _capi.block_cached_workspace_size(4, 64, 672, 32, 32, 128)
+    ws = _capi.block_cached_workspace_size(2, 32, 4128, 32, 32, 128)
     assert ws > 0 and ws % 4 == 0
     assert _capi.select_workspace_size(4, 1216, 32, 32, 128, True) >= 4 * 32 * 128 * 2 + 4 * 32 * 1216 * 2
     assert _capi.select_workspace_size(0, 10, 32, 32, 128, True) == 0
@@ -61,7 +61,9 @@ def test_argument_validation_without_gpu():
     assert rc == _capi.DLLM_ERR_INVALID_ARG and "aligned" in msg
     assert lib.dllm_attn_varlen_fwd(fake, fake, fake, fake, fake, fake, None, 0, 8, 8, 4, 4, 128,
                                     512, 512, 512, 512, 0.1, None) == 0   # nothing to do
-    rc, msg = _err(lib.dllm_attn_block_cached_fwd(fake, fake, fake, fake, fake, None, 4, 64, 672, fake, fake,
+    # two 32-row blocks against 4096 cached rows split over the keys and need a workspace
+    assert _capi.block_cached_workspace_size(2, 32, 4128, 32, 32, 128) > 0
+    rc, msg = _err(lib.dllm_attn_block_cached_fwd(fake, fake, fake, fake, fake, None, 2, 32, 4128, fake, fake,
                                                   4096, fake, fake, 32, 32, 128, 4096, 4096, 4096, 4096, 0.1,
                                                   None, 0, None))
     assert rc == _capi.DLLM_ERR_WORKSPACE

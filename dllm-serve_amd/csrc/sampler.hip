@@ -1,0 +1,351 @@
+// K8 / K9: the low-confidence remasking sampler of the diffusion runner.
+//
+// K8 (smx_partial_kernel + smx_final_kernel) reduces each row of bf16 logits
+// [M, V] to what `x0_p, x0 = torch.max(F.softmax(logits, -1), -1)` returns
+// (dllmserve/engine/model_runner.py:862-863,886-887):
+//   m  = max_j l_j,  s = sum_j exp(l_j - m)                      (f32)
+//   P_j = bf16(exp(l_j - m) / s)                                  (the bf16 probabilities)
+//   x0_p = max_j P_j = bf16(1 / s),  x0 = min { j : P_j == x0_p }
+// in one read of the logits.  A probability can only round to x0_p when its
+// logit is within 2^-6 of m, and bf16 logits below m are that close to it
+// only when |m| <= 2; so x0 is the first index of the maximal logit unless
+// |m| <= 2, in which case the final kernel rescans the columns before that
+// index for an earlier one whose rounded probability ties.
+//
+// Layout: one workgroup reduces `split` consecutive 16-byte chunks of one row
+// (each thread every 256th chunk, four loads in flight) to a record
+// {m, s, first index of m}; the final kernel merges a row's records in one
+// wavefront.  HBM-bound: 2 V bytes per row, read once.
+//
+// K9 (lowconf_unmask_kernel) is the per-sequence unmasking step that follows
+// (model_runner.py:895-949): in the sequence's window of token positions,
+// count the masked ones, unmask k = min(ceil(nmask / steps_remain), nmask) of
+// them -- the window's first position first when the first-token rule
+// applies -- and the rest in order of confidence (descending, ties to the
+// lower position, which is the set torch.topk returns).  One workgroup per
+// sequence; the k-th largest (confidence, position) key is found by a
+// bitwise search over keys held in LDS.
+#include "common.h"
+
+#include <limits.h>
+
+namespace dllm {
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kSmxThreads = 256;
+constexpr int kUnmaskMaxWin = 8192;  // SamplingParams caps gen_length at 8192
+
+struct SmxRec {
+  float m;
+  float s;
+  int32_t i;
+  int32_t pad;
+};
+
+__device__ __forceinline__ float fexp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Merge partial (m2, s2, i2) into (m, s, i).  An empty partial is
+// (-inf, 0, INT_MAX).  Symmetric, so butterfly reductions agree on all lanes.
+__device__ __forceinline__ void smx_merge(float& m, float& s, int& i, float m2, float s2, int i2) {
+  const float mn = fmaxf(m, m2);
+  const float a = (m == mn) ? s : s * fexp2((m - mn) * kLog2e);
+  const float b = (m2 == mn) ? s2 : s2 * fexp2((m2 - mn) * kLog2e);
+  i = (m > m2) ? i : (m2 > m) ? i2 : min(i, i2);
+  s = a + b;
+  m = mn;
+}
+
+__device__ __forceinline__ void smx_wave_reduce(float& m, float& s, int& i) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float m2 = __shfl_xor(m, off);
+    const float s2 = __shfl_xor(s, off);
+    const int i2 = __shfl_xor(i, off);
+    smx_merge(m, s, i, m2, s2, i2);
+  }
+}
+
+// Fold 8 logits (one 16-byte chunk starting at column e0) into the running
+// (m, s, i).  A thread's chunks arrive in increasing column order, so a tie
+// with the running max keeps the earlier index.
+__device__ __forceinline__ void smx_chunk(u32x4_t v, int e0, float& m, float& s, int& i) {
+  float f[8];
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    f[2 * w] = __uint_as_float(v[w] << 16);
+    f[2 * w + 1] = __uint_as_float(v[w] & 0xffff0000u);
+  }
+  const float cm = fmaxf(fmaxf(fmaxf(f[0], f[1]), fmaxf(f[2], f[3])), fmaxf(fmaxf(f[4], f[5]), fmaxf(f[6], f[7])));
+  if (cm > m) {
+    int k = 7;
+#pragma unroll
+    for (int kk = 6; kk >= 0; --kk)
+      if (f[kk] == cm) k = kk;
+    s *= fexp2((m - cm) * kLog2e);
+    m = cm;
+    i = e0 + k;
+  }
+  if (m != -INFINITY) {
+    float e[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) e[k] = fexp2((f[k] - m) * kLog2e);
+    s += ((e[0] + e[1]) + (e[2] + e[3])) + ((e[4] + e[5]) + (e[6] + e[7]));
+  }
+}
+
+struct SmxArgs {
+  const uint16_t* logits;
+  int64_t ld;       // elements between rows
+  int M;
+  int V;
+  int chunks;       // V / 8
+  int split;        // chunks per workgroup
+  int S;            // workgroups per row
+  SmxRec* part;     // [M][S]
+  int64_t* x0;
+  uint16_t* x0p;
+};
+
+__global__ __launch_bounds__(kSmxThreads) void smx_partial_kernel(SmxArgs a) {
+  __shared__ float red_m[kSmxThreads / 64];
+  __shared__ float red_s[kSmxThreads / 64];
+  __shared__ int red_i[kSmxThreads / 64];
+  const int row = blockIdx.x / a.S;
+  const int sp = blockIdx.x - row * a.S;
+  const int c0 = sp * a.split;
+  const int c1 = min(a.chunks, c0 + a.split);
+  const uint16_t* base = a.logits + (int64_t)row * a.ld;
+  float m = -INFINITY, s = 0.f;
+  int idx = INT_MAX;
+  const u32x4_t ninf = {0xff80ff80u, 0xff80ff80u, 0xff80ff80u, 0xff80ff80u};
+  for (int c = c0 + (int)threadIdx.x; c < c1; c += 4 * kSmxThreads) {
+    u32x4_t v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int cc = c + u * kSmxThreads;
+      v[u] = cc < c1 ? ld128_stream(base + 8 * (int64_t)cc) : ninf;
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) smx_chunk(v[u], 8 * (c + u * kSmxThreads), m, s, idx);
+  }
+  smx_wave_reduce(m, s, idx);
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    red_m[wave] = m;
+    red_s[wave] = s;
+    red_i[wave] = idx;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < kSmxThreads / 64; ++w) smx_merge(m, s, idx, red_m[w], red_s[w], red_i[w]);
+    SmxRec r;
+    r.m = m;
+    r.s = s;
+    r.i = idx;
+    r.pad = 0;
+    a.part[(int64_t)row * a.S + sp] = r;
+  }
+}
+
+// One wavefront per row: merge the row's records, then resolve ties of the
+// rounded probabilities when |m| <= 2.
+__global__ __launch_bounds__(256) void smx_final_kernel(SmxArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= a.M) return;  // uniform per wavefront
+  float m = -INFINITY, s = 0.f;
+  int idx = INT_MAX;
+  for (int k = lane; k < a.S; k += 64) {
+    const SmxRec r = a.part[(int64_t)row * a.S + k];
+    smx_merge(m, s, idx, r.m, r.s, r.i);
+  }
+  smx_wave_reduce(m, s, idx);
+  const uint32_t P = f32_to_bf16_bits(1.0f / s);
+  int best = idx;
+  if (fabsf(m) <= 2.0f && idx != INT_MAX && idx > 0) {
+    // earliest column j < idx with bf16(exp(l_j - m) / s) == P
+    const uint16_t* base = a.logits + (int64_t)row * a.ld;
+    const float thr = m - 0.015625f;
+    int found = INT_MAX;
+    const int nch = (idx + 7) >> 3;
+    for (int c = lane; c < nch; c += 64) {
+      const u32x4_t v = ld128(base + 8 * (int64_t)c);
+#pragma unroll
+      for (int k = 7; k >= 0; --k) {
+        const uint32_t w = v[k >> 1];
+        const float f = (k & 1) ? __uint_as_float(w & 0xffff0000u) : __uint_as_float(w << 16);
+        const int j = 8 * c + k;
+        if (j < idx && f >= thr && f32_to_bf16_bits(expf(f - m) / s) == P) found = min(found, j);
+      }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) found = min(found, __shfl_xor(found, off));
+    best = min(best, found);
+  }
+  if (lane == 0) {
+    a.x0[row] = best == INT_MAX ? 0 : best;
+    a.x0p[row] = (uint16_t)P;
+  }
+}
+
+// ---- K9 ---------------------------------------------------------------------
+
+struct UnmaskArgs {
+  int64_t* tokens;
+  int64_t n_tokens;       // elements of tokens (bounds guard)
+  const int32_t* params;  // [n_seq][5]: tok_off, win_len, row_off, steps_remain, first_rule
+  const int64_t* x0;
+  const uint16_t* conf;
+  int64_t n_rows;         // rows of x0 / conf (bounds guard)
+  int64_t mask_id;
+  int max_win;
+  int32_t* n_unmasked;    // nullable
+};
+
+// Order-preserving map of bf16 bits to 16-bit unsigned (-0 equals +0).
+__device__ __forceinline__ uint32_t conf_order(uint32_t b) {
+  if (b == 0x8000u) b = 0;
+  return (b & 0x8000u) ? (~b & 0xffffu) : (b | 0x8000u);
+}
+
+__device__ __forceinline__ int block_sum(int v, int* red) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return red[0] + red[1] + red[2] + red[3];
+}
+
+__global__ __launch_bounds__(256) void lowconf_unmask_kernel(UnmaskArgs a) {
+  __shared__ uint32_t keys[kUnmaskMaxWin];
+  __shared__ int red[4];
+  const int b = blockIdx.x;
+  const int32_t* p = a.params + 5 * (int64_t)b;
+  const int64_t tok_off = p[0];
+  const int n = min(min(p[1], a.max_win), kUnmaskMaxWin);
+  const int64_t r0 = p[2];
+  const int sr = p[3];
+  const bool first_rule = p[4] != 0;
+  const int tid = threadIdx.x;
+  const bool valid = n > 0 && tok_off >= 0 && tok_off + n <= a.n_tokens && r0 >= 0 && r0 + n <= a.n_rows;
+  if (!valid) {  // uniform per workgroup
+    if (a.n_unmasked && tid == 0) a.n_unmasked[b] = 0;
+    return;
+  }
+  int64_t* tok = a.tokens + tok_off;
+  int cnt = 0;
+  for (int j = tid; j < n; j += 256) {
+    const bool masked = tok[j] == a.mask_id;
+    keys[j] = masked ? ((conf_order(a.conf[r0 + j]) << 16) | (0xffffu - (uint32_t)j)) : 0u;
+    cnt += masked;
+  }
+  const int nmask = block_sum(cnt, red);  // its barriers also publish keys[]
+  // steps_remain <= 0: nothing is unmasked (the reference divides by it)
+  int k = sr > 0 ? min((nmask + sr - 1) / sr, nmask) : 0;
+  const int k_total = k;
+  if (first_rule && k > 0 && keys[0] != 0u) {
+    __syncthreads();  // every thread has read keys[0]
+    if (tid == 0) {
+      tok[0] = a.x0[r0];
+      keys[0] = 0u;
+    }
+    --k;
+    __syncthreads();
+  }
+  if (k > 0) {
+    uint32_t T = 0;
+    for (int bit = 31; bit >= 0; --bit) {
+      const uint32_t cand = T | (1u << bit);
+      int c = 0;
+      for (int j = tid; j < n; j += 256) c += keys[j] >= cand;
+      if (block_sum(c, red) >= k) T = cand;
+    }
+    // keys are distinct and the k-th largest is non-zero: exactly k pass
+    for (int j = tid; j < n; j += 256)
+      if (keys[j] >= T) tok[j] = a.x0[r0 + j];
+  }
+  if (a.n_unmasked && tid == 0) a.n_unmasked[b] = k_total;
+}
+
+}  // namespace dllm
+
+using namespace dllm;
+
+static int smx_splits(int M, int chunks) {
+  // about 8 workgroups per CU in all, each at least 256 chunks (4 KiB)
+  const int want = (2048 + M - 1) / M;
+  const int cap = chunks / kSmxThreads > 1 ? chunks / kSmxThreads : 1;
+  int S = want < cap ? want : cap;
+  if (S > 64) S = 64;
+  if (S < 1) S = 1;
+  return S;
+}
+
+extern "C" size_t dllm_softmax_max_workspace_size(int M, int V) {
+  if (M <= 0 || V <= 0) return 0;
+  const int S = smx_splits(M, (V + 7) / 8);
+  return (size_t)M * S * sizeof(SmxRec);
+}
+
+extern "C" int dllm_softmax_max(const uint16_t* logits, int64_t ld, int M, int V, int64_t* x0, uint16_t* x0_p,
+                                void* workspace, size_t workspace_bytes, void* stream) {
+  static const char* name = "dllm_softmax_max";
+  if (M < 0 || V < 0) return fail(DLLM_ERR_INVALID_ARG, "%s: negative size", name);
+  if (M == 0) return DLLM_OK;
+  if (V == 0 || V % 8 != 0)
+    return fail(DLLM_ERR_UNSUPPORTED, "%s: vocabulary size %d must be a positive multiple of 8", name, V);
+  if (!logits || !x0 || !x0_p) return fail(DLLM_ERR_INVALID_ARG, "%s: null pointer", name);
+  if (!aligned16(logits) || ld % 8 != 0 || ld < V)
+    return fail(DLLM_ERR_INVALID_ARG, "%s: logits must be 16-byte aligned with a row stride >= V and a multiple of 8",
+                name);
+  const int chunks = V / 8;
+  const int S = smx_splits(M, chunks);
+  const size_t need = (size_t)M * S * sizeof(SmxRec);
+  if (!workspace || workspace_bytes < need || !aligned16(workspace))
+    return fail(DLLM_ERR_WORKSPACE, "%s: workspace of %zu bytes (16-byte aligned) required, got %zu", name, need,
+                workspace ? workspace_bytes : (size_t)0);
+  if ((int64_t)M * S > INT_MAX) return fail(DLLM_ERR_INVALID_ARG, "%s: too many rows", name);
+  SmxArgs a;
+  a.logits = logits;
+  a.ld = ld;
+  a.M = M;
+  a.V = V;
+  a.chunks = chunks;
+  a.S = S;
+  a.split = (chunks + S - 1) / S;
+  a.part = reinterpret_cast<SmxRec*>(workspace);
+  a.x0 = x0;
+  a.x0p = x0_p;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  smx_partial_kernel<<<dim3((unsigned)(M * S)), dim3(kSmxThreads), 0, st>>>(a);
+  int rc = check_launch(name);
+  if (rc != DLLM_OK) return rc;
+  smx_final_kernel<<<dim3((unsigned)((M + 3) / 4)), dim3(256), 0, st>>>(a);
+  return check_launch(name);
+}
+
+extern "C" int dllm_lowconf_unmask(int64_t* tokens, int64_t n_tokens, const int32_t* seq_params, int n_seq,
+                                   int max_win, const int64_t* x0, const uint16_t* conf, int64_t n_rows,
+                                   int64_t mask_id, int32_t* n_unmasked, void* stream) {
+  static const char* name = "dllm_lowconf_unmask";
+  if (n_seq < 0 || max_win < 0 || n_tokens < 0 || n_rows < 0)
+    return fail(DLLM_ERR_INVALID_ARG, "%s: negative size", name);
+  if (n_seq == 0) return DLLM_OK;
+  if (max_win > kUnmaskMaxWin)
+    return fail(DLLM_ERR_UNSUPPORTED, "%s: window of %d positions exceeds %d", name, max_win, kUnmaskMaxWin);
+  if (!tokens || !seq_params || (n_rows > 0 && (!x0 || !conf)))
+    return fail(DLLM_ERR_INVALID_ARG, "%s: null pointer", name);
+  UnmaskArgs a;
+  a.tokens = tokens;
+  a.n_tokens = n_tokens;
+  a.params = seq_params;
+  a.x0 = x0;
+  a.conf = conf;
+  a.n_rows = n_rows;
+  a.mask_id = mask_id;
+  a.max_win = max_win;
+  a.n_unmasked = n_unmasked;
+  lowconf_unmask_kernel<<<dim3((unsigned)n_seq), dim3(256), 0, reinterpret_cast<hipStream_t>(stream)>>>(a);
+  return check_launch(name);
+}

@@ -52,6 +52,9 @@ SIGNATURES = {
          _P, _P, _I64, _P, _P, _P, _SZ, _P],
     ),
     "dllm_rope_neox": (_I, [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _P, _I64, _I, _I, _I, _I, _P]),
+    "dllm_softmax_max_workspace_size": (_SZ, [_I, _I]),
+    "dllm_softmax_max": (_I, [_P, _I64, _I, _I, _P, _P, _P, _SZ, _P]),
+    "dllm_lowconf_unmask": (_I, [_P, _I64, _P, _I, _I, _P, _P, _I64, _I64, _P, _P]),
 }
 
 _lib = None
@@ -197,3 +200,30 @@ def rope_neox(q_in, q_out, k_in, k_out, positions, cos_sin_cache, n_tok, Hq, Hkv
         positions.data_ptr(), cos_sin_cache.data_ptr(), cos_sin_cache.shape[0],
         n_tok, Hq, Hkv, D, _stream(positions.device))
     _check(rc, "dllm_rope_neox")
+
+
+def softmax_max_workspace_size(M, V) -> int:
+    return int(load().dllm_softmax_max_workspace_size(M, V))
+
+
+def softmax_max(logits, x0, x0_p, workspace):
+    """K8: x0_p, x0 = max(softmax(logits, -1), -1) of bf16 logits [M, V]
+    (x0 int64 [M], x0_p bf16 [M])."""
+    _require_gpu(logits, x0, x0_p, workspace)
+    lib = load()
+    M, V = logits.shape
+    ws_bytes = workspace.numel() * workspace.element_size()
+    rc = lib.dllm_softmax_max(logits.data_ptr(), logits.stride(0), M, V, x0.data_ptr(), x0_p.data_ptr(),
+                              workspace.data_ptr(), ws_bytes, _stream(logits.device))
+    _check(rc, "dllm_softmax_max")
+
+
+def lowconf_unmask(tokens, seq_params, n_seq, max_win, x0, conf, mask_id, n_unmasked=None):
+    """K9: one low-confidence unmasking step of n_seq windows of the flat
+    int64 token array (seq_params: int32 [n_seq, 5], see include/dllm_attn.h)."""
+    _require_gpu(tokens, seq_params, x0, conf, n_unmasked)
+    lib = load()
+    rc = lib.dllm_lowconf_unmask(tokens.data_ptr(), tokens.numel(), seq_params.data_ptr(), n_seq, max_win,
+                                 x0.data_ptr(), conf.data_ptr(), x0.numel(), int(mask_id), _ptr(n_unmasked),
+                                 _stream(tokens.device))
+    _check(rc, "dllm_lowconf_unmask")

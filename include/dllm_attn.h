@@ -187,6 +187,51 @@ int dllm_rope_neox(const dllm_bf16* q_in, int64_t q_in_stride, dllm_bf16* q_out,
                    const int64_t* positions, const float* cos_sin_cache, int64_t max_position,
                    int n_tok, int Hq, int Hkv, int D, void* stream);
 
+/*
+ * K8 -- softmax-max of logit rows.  Replaces
+ *   probs = F.softmax(logits, dim=-1); x0_p, x0 = torch.max(probs, dim=-1)
+ * on bf16 logits (dllmserve/engine/model_runner.py:862-863,886-887, the
+ * low-confidence branch of _reconstruct_and_sample_optimized_v2; also :697-701).
+ *
+ * logits is [M, V] bf16 with row stride ld elements.  Per row, in f32:
+ *   m = max_j l_j,  s = sum_j exp(l_j - m),  P_j = bf16(exp(l_j - m) / s)
+ *   x0_p[r] = max_j P_j = bf16(1 / s),  x0[r] = min { j : P_j == x0_p[r] }
+ * (torch.max returns the first maximal index).  Rows holding NaN or only
+ * -inf give unspecified results (torch's are NaN).  V must be a multiple of
+ * 8; logits 16-byte aligned, ld a multiple of 8 and >= V.  workspace must
+ * hold dllm_softmax_max_workspace_size(M, V) bytes, 16-byte aligned.
+ */
+size_t dllm_softmax_max_workspace_size(int M, int V);
+int dllm_softmax_max(const dllm_bf16* logits, int64_t ld, int M, int V, int64_t* x0, dllm_bf16* x0_p,
+                     void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * K9 -- low-confidence unmasking of one denoising step.  Replaces the
+ * per-sequence loop of _reconstruct_and_sample_optimized_v2
+ * (dllmserve/engine/model_runner.py:895-949: mask test, steps_remain,
+ * num_to_unmask, the is_full_attention first-token rule, torch.topk and the
+ * token write-back).
+ *
+ * seq_params is int32 [n_seq][5]: {tok_off, win_len, row_off, steps_remain,
+ * first_rule}.  Sequence b's window is tokens[tok_off + j], j in [0, win_len)
+ * (the positions the reference's `indices` name); its predictions and
+ * confidences are x0[row_off + j] and conf[row_off + j] (conf: x0_p from
+ * dllm_softmax_max for "low_confidence", or the caller's uniform draws for
+ * "random", :903-907).  With nmask = #{j : tokens[tok_off + j] == mask_id}:
+ *   k = min(ceil(nmask / steps_remain), nmask)     (0 when steps_remain <= 0)
+ *   if first_rule and k > 0 and position 0 is masked: it takes x0[row_off]
+ *     and k -= 1 (:917-935)
+ *   the k masked positions with the highest conf (ties: lower j first, the
+ *   set torch.topk returns) take their x0.
+ * n_unmasked (nullable) receives the k of each sequence before the
+ * first-token rule.  A sequence whose window or rows fall outside
+ * [0, n_tokens) / [0, n_rows) is left unchanged (n_unmasked 0).  max_win must
+ * bound every win_len and be at most 8192 (the reference's gen_length cap).
+ */
+int dllm_lowconf_unmask(int64_t* tokens, int64_t n_tokens, const int32_t* seq_params, int n_seq, int max_win,
+                        const int64_t* x0, const dllm_bf16* conf, int64_t n_rows, int64_t mask_id,
+                        int32_t* n_unmasked, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

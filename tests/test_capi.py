@@ -107,3 +107,44 @@ def test_rope_module_refuses_cpu_tensors():
     q = torch.zeros(4, 2 * 128, dtype=torch.bfloat16)
     with pytest.raises(RuntimeError, match="GPU only"):
         rope(torch.arange(4), q, q.clone())
+
+
+def test_sampler_validation_without_gpu():
+    lib = _capi.load()
+    P = ctypes.c_void_p
+    fake = P(4096)
+    assert _capi.softmax_max_workspace_size(1024, 126464) == 1024 * 2 * 16
+    assert _capi.softmax_max_workspace_size(64, 126464) == 64 * 32 * 16
+    assert _capi.softmax_max_workspace_size(0, 126464) == 0
+    ws = _capi.softmax_max_workspace_size(64, 126464)
+    rc, msg = _err(lib.dllm_softmax_max(fake, 126464, 64, 126460, fake, fake, fake, ws, None))
+    assert rc == _capi.DLLM_ERR_UNSUPPORTED and "multiple of 8" in msg
+    rc, msg = _err(lib.dllm_softmax_max(fake, 126456, 64, 126464, fake, fake, fake, ws, None))
+    assert rc == _capi.DLLM_ERR_INVALID_ARG and "stride" in msg
+    rc, msg = _err(lib.dllm_softmax_max(fake, 126464, 64, 126464, fake, fake, fake, ws - 16, None))
+    assert rc == _capi.DLLM_ERR_WORKSPACE and "workspace" in msg
+    assert lib.dllm_softmax_max(fake, 126464, 0, 126464, fake, fake, None, 0, None) == 0
+    rc, msg = _err(lib.dllm_lowconf_unmask(fake, 100, fake, 4, 8193, fake, fake, 100, 126336, None, None))
+    assert rc == _capi.DLLM_ERR_UNSUPPORTED and "8192" in msg
+    assert lib.dllm_lowconf_unmask(fake, 100, fake, 0, 10, fake, fake, 100, 126336, None, None) == 0
+
+
+def test_sampler_refuses_cpu_tensors():
+    import torch
+    from dllm_serve_amd.engine.sampler import RemaskSampler, step_windows
+    from dllm_serve_amd.engine.sequence import Sequence
+    from dllm_serve_amd.sparse.state import SparseConfig
+
+    seqs = [Sequence([1] * 10, 8, 99, None, device="cpu", steps=4),
+            Sequence([2] * 6, 8, 99, SparseConfig(default_block_len=4), device="cpu")]
+    # (hidden row, window start, length, steps_remain, first-token rule)
+    assert step_windows(seqs) == [(10, 10, 8, 4, 0), (18 + 6, 6, 4, 4, 1)]
+    seqs[0].current_step = 4
+    with pytest.raises(ZeroDivisionError):
+        step_windows(seqs)
+    seqs[0].current_step = 0
+    s = RemaskSampler(lambda h: h, 99)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        s(torch.zeros(32, 8, dtype=torch.bfloat16), seqs, torch.zeros(2, 18, dtype=torch.int64))
+    with pytest.raises(NotImplementedError):
+        s(torch.zeros(32, 8, dtype=torch.bfloat16), seqs, torch.zeros(2, 18, dtype=torch.int64), temperature=1.0)

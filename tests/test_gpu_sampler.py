@@ -1,0 +1,172 @@
+"""K8 (softmax-max of logit rows) and K9 (low-confidence unmasking) on the
+GPU, through the C ABI, against the oracle (oracle/sampler.py).
+
+x0 must equal the oracle's index on every row whose result does not depend
+on the summation order of s (the oracle evaluated with s scaled by 1 +- 4e-6
+agrees); that is all rows but a handful, and the test requires >= 99 %.  x0_p
+is bf16(1/s): within one bf16 unit everywhere and equal on >= 98 % of rows.
+The unmasking kernel is bit-exact against the oracle given the same
+predictions and confidences."""
+import numpy as np
+import pytest
+import torch
+
+from helpers import bits
+
+from oracle import sampler as osm
+from oracle.bf16 import f32_to_bf16_bits
+from dllm_serve_amd import _capi
+
+pytestmark = pytest.mark.gpu
+
+MASK = 126336
+
+
+def _run_k8(logits):
+    M, V = logits.shape
+    x0 = torch.full((M,), -1, dtype=torch.int64, device=logits.device)
+    p = torch.zeros(M, dtype=torch.bfloat16, device=logits.device)
+    ws = torch.empty(max(16, _capi.softmax_max_workspace_size(M, V)), dtype=torch.uint8, device=logits.device)
+    _capi.softmax_max(logits, x0, p, ws)
+    torch.cuda.synchronize()
+    return x0.cpu().numpy(), bits(p)
+
+
+def _check_k8(logits_host_bits, x0, p):
+    ox0, op = osm.softmax_max(logits_host_bits)
+    lo0, _ = osm.softmax_max(logits_host_bits, 1 - 4e-6)
+    hi0, _ = osm.softmax_max(logits_host_bits, 1 + 4e-6)
+    robust = (lo0 == ox0) & (hi0 == ox0)
+    assert robust.mean() >= 0.99
+    bad = np.nonzero(robust & (x0 != ox0))[0]
+    assert bad.size == 0, f"x0 differs on rows {bad[:8]}: got {x0[bad[:8]]} want {ox0[bad[:8]]}"
+    d = np.abs(p.astype(np.int32) - op.astype(np.int32))
+    assert d.max() <= 1 and np.mean(d == 0) >= 0.98, f"x0_p: max diff {d.max()}, equal {np.mean(d == 0):.4f}"
+
+
+@pytest.mark.parametrize("M,V,sigma,pad", [
+    (64, 126464, 1.3, 0),       # LLaDA vocabulary, logits of the random-weight model's scale
+    (256, 126464, 3.0, 8),      # C2 cached step row count, strided rows
+    (1024, 126464, 1.3, 0),     # C2 dense step row count
+    (96, 152064, 2.0, 0),       # Dream vocabulary
+    (300, 4096, 0.3, 0),        # |max| <= 2: the rounding-tie rescan runs on every row
+    (37, 264, 0.5, 8),
+    (5, 8, 1.0, 0),
+])
+def test_softmax_max_matches_oracle(dev, M, V, sigma, pad):
+    print(f"softmax_max M={M} V={V} sigma={sigma} pad={pad}", flush=True)
+    g = torch.Generator().manual_seed(M * 7 + V)
+    full = (torch.randn(M, V + pad, generator=g) * sigma).to(torch.bfloat16)
+    full[:, V:] = 100.0                              # padding columns must be ignored
+    logits = full.to(dev)[:, :V]
+    x0, p = _run_k8(logits)
+    _check_k8(bits(full[:, :V]), x0, p)
+
+
+def test_softmax_max_ties_and_neg_inf(dev):
+    print("softmax_max ties / -inf", flush=True)
+    V = 126464
+    g = torch.Generator().manual_seed(3)
+    rows = (torch.randn(6, V, generator=g) * 1.5)
+    rows[0, [5000, 17, 90000]] = 9.0                 # exact ties of the maximum: first index
+    rows[1, :] = 0.75                                # uniform row: index 0
+    rows[2, ::3] = -float("inf")                     # -inf columns
+    rows[3, 100000:] = -float("inf")
+    rows[3, 126463] = -float("inf")
+    rows[4, :] = 0.28125                             # rounding tie: index 3 beats index 10
+    rows[4, 3], rows[4, 10] = 1.0 - 2 ** -8, 1.0
+    rows[5, 126463] = 12.0                           # maximum in the very last column
+    t = rows.to(torch.bfloat16)
+    x0, p = _run_k8(t.to(dev))
+    ox0, op = osm.softmax_max(bits(t))
+    assert x0[0] == 17 and x0[1] == 0 and x0[4] == 3 and x0[5] == 126463
+    assert np.array_equal(x0, ox0)
+    assert np.all(np.abs(p.astype(np.int32) - op.astype(np.int32)) <= 1)
+
+
+def _unmask_case(rng, n_seq, max_win, tie_levels):
+    tokens, params, rows = [], [], 0
+    for b in range(n_seq):
+        n = int(rng.integers(0, max_win + 1))
+        pad = int(rng.integers(0, 9))
+        tok = rng.integers(0, 1000, n + pad)
+        tok[pad:][rng.random(n) < rng.random()] = MASK
+        params.append((len(tokens) + pad, n, rows, int(rng.integers(-1, 9)), int(rng.random() < 0.5)))
+        tokens.extend(tok.tolist())
+        rows += n
+    conf = f32_to_bf16_bits(np.round(rng.random(rows) * tie_levels) / tie_levels) if tie_levels else \
+        f32_to_bf16_bits(rng.random(rows).astype(np.float32))
+    x0 = rng.integers(1000, 126000, rows)
+    return np.array(tokens, np.int64), params, conf, x0
+
+
+@pytest.mark.parametrize("n_seq,max_win,ties", [(64, 300, 0), (64, 300, 16), (8, 8192, 64), (3, 1, 0), (32, 64, 2)])
+def test_unmask_matches_oracle(dev, n_seq, max_win, ties):
+    print(f"unmask n_seq={n_seq} max_win={max_win} ties={ties}", flush=True)
+    rng = np.random.default_rng(n_seq * 31 + max_win + ties)
+    tokens, params, conf, x0 = _unmask_case(rng, n_seq, max_win, ties)
+    want, want_n = osm.unmask_step(tokens, params, x0, conf, MASK)
+    t = torch.from_numpy(tokens).to(dev)
+    p = torch.tensor(params, dtype=torch.int32).to(dev)
+    cf = torch.from_numpy(conf.view(np.int16)).view(torch.bfloat16).to(dev)
+    xd = torch.from_numpy(x0).to(dev)
+    nun = torch.full((n_seq,), -1, dtype=torch.int32, device=dev)
+    _capi.lowconf_unmask(t, p, n_seq, max(w[1] for w in params), xd, cf, MASK, nun)
+    torch.cuda.synchronize()
+    got = t.cpu().numpy()
+    assert np.array_equal(nun.cpu().numpy(), want_n)
+    bad = np.nonzero(got != want)[0]
+    assert bad.size == 0, f"{bad.size} tokens differ, first at {bad[:8]}"
+
+
+def test_remask_sampler_step_matches_oracle(dev):
+    """RemaskSampler on a mixed batch (no SparseConfig, and sparse sequences
+    in the full-attention, compute-cache and reuse states): LM head by torch
+    (a library GEMM), K8 + K9 against the oracle on the same logits."""
+    from dllm_serve_amd.engine.sampler import RemaskSampler, step_windows
+    from dllm_serve_amd.engine.sequence import Sequence
+    from dllm_serve_amd.sparse.state import SparseConfig
+
+    print("remask sampler step", flush=True)
+    H, V = 512, 126464
+    g = torch.Generator().manual_seed(21)
+    w = (torch.randn(V, H, generator=g) * 0.05).to(torch.bfloat16).to(dev)
+    cfg = SparseConfig(enabled=True, default_block_len=32, retention_ratio=0.5, delay_step=1)
+    seqs = [Sequence([1] * 40, 64, MASK, None, device=dev, steps=16),
+            Sequence([2] * 50, 64, MASK, cfg, device=dev),
+            Sequence([3] * 30, 70, MASK, cfg, device=dev),
+            Sequence([4] * 20, 32, MASK, cfg, device=dev)]
+    seqs[0].current_step = 5
+    seqs[2].advance()                                 # compute-cache state
+    for _ in range(2):
+        seqs[3].advance()                             # reuse state
+    # partly unmasked windows
+    N = max(s.num_tokens for s in seqs)
+    host = np.zeros((len(seqs), N), np.int64)
+    rng = np.random.default_rng(4)
+    for b, s in enumerate(seqs):
+        tok = np.array(s.token_ids)
+        tok[s.num_prompt_tokens:][rng.random(s.gen_length) < 0.3] = 777
+        host[b, :s.num_tokens] = tok
+    tokens = torch.from_numpy(host).to(dev)
+    n_rows = sum(s.step_rows()[1] for s in seqs)
+    hidden = torch.randn(n_rows, H, generator=g).to(torch.bfloat16).to(dev)
+    sampler = RemaskSampler(lambda h: h @ w.t(), MASK, max_logprobs=64)
+    nun = sampler(hidden, seqs, tokens)
+    torch.cuda.synchronize()
+    # oracle on the same logits
+    win = step_windows(seqs)
+    sel = torch.cat([torch.arange(h0, h0 + n) for h0, _, n, _, _ in win]).to(dev)
+    rows = hidden.index_select(0, sel)
+    logits = torch.cat([rows[a:a + 64] @ w.t() for a in range(0, rows.shape[0], 64)])  # the sampler's chunks
+    lb = bits(logits)
+    x0, p = _run_k8(logits)
+    _check_k8(lb, x0, p)
+    params, r = [], 0
+    for b, (h0, lo, n, sr, first) in enumerate(win):
+        params.append((b * N + lo, n, r, sr, first))
+        r += n
+    want, want_n = osm.unmask_step(host.reshape(-1), params, x0, p, MASK)
+    assert np.array_equal(nun.cpu().numpy(), want_n)
+    assert np.array_equal(tokens.cpu().numpy().reshape(-1), want)
+    assert want_n.sum() > 0

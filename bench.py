@@ -324,9 +324,11 @@ class LLaDA8B:
 def denoise(model, batch, prompt, gen, steps, block, sparse, dev, seed=0, ratio=1.0, head_select=True):
     """Generate `gen` tokens for `batch` random prompts; returns (seconds, steps).
 
-    Token ids stay on the device; each step unmasks ceil(masked / remaining
-    steps) positions per sequence (over all generated rows when dense, over
-    the current block when cached), picked by confidence = max softmax prob."""
+    Token ids stay on the device; each step's LM head runs on the rows that
+    may be unmasked (all generated rows when dense, the current block when
+    cached) and RemaskSampler unmasks ceil(masked / remaining steps) of them
+    by confidence = max softmax probability (K8 + K9, no host round trip)."""
+    from dllm_serve_amd.engine.sampler import RemaskSampler
     from dllm_serve_amd.engine.sequence import PageAllocator, Sequence, prepare_step
     from dllm_serve_amd.sparse.state import SparseConfig
     from dllm_serve_amd.utils.context import reset_context
@@ -344,8 +346,7 @@ def denoise(model, batch, prompt, gen, steps, block, sparse, dev, seed=0, ratio=
         for s in seqs:
             alloc.allocate(s)
     tok = torch.tensor([s.token_ids for s in seqs], dtype=torch.int64, device=dev)  # [B, N]
-    n_masked = [gen] * batch          # masked rows left in the denoising window (host bookkeeping)
-    block_seen = [0] * batch
+    sampler = RemaskSampler(lambda h: h @ model.lm_head.t(), c["mask_id"])
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
@@ -355,32 +356,7 @@ def denoise(model, batch, prompt, gen, steps, block, sparse, dev, seed=0, ratio=
         prepare_step(seqs, dev, build_inputs=False)  # Context: cu_seqlens, slot lists, seqs
         hidden = model.forward(ids, pos)
         reset_context()
-        spans, off = [], 0
-        for i, (s, (a, n)) in enumerate(zip(seqs, rows)):
-            if s.sparse_state is None:
-                lo, hi, remain = s.num_prompt_tokens, s.num_tokens, s.steps - s.current_step
-            else:
-                st = s.sparse_state
-                bs, bl = st.block_span(s.num_prompt_tokens, s.num_tokens)
-                if st.current_block_idx != block_seen[i] or s.current_step == 0:
-                    block_seen[i] = st.current_block_idx
-                    n_masked[i] = bl
-                lo, hi, remain = bs, bs + bl, max(1, bl - st.step_in_block)
-            k = min(-(-n_masked[i] // max(1, remain)), n_masked[i])
-            n_masked[i] -= k
-            spans.append((off + lo - a, off + hi - a, lo, hi, k))
-            off += n
-        sel = torch.cat([hidden[x0:x1] for x0, x1, _, _, _ in spans])
-        p, x0 = torch.softmax((sel @ model.lm_head.t()).float(), dim=-1).max(dim=-1)
-        o = 0
-        for i, (_, _, lo, hi, k) in enumerate(spans):
-            m = hi - lo
-            if k > 0:
-                masked = tok[i, lo:hi] == c["mask_id"]
-                conf = torch.where(masked, p[o:o + m], torch.full_like(p[o:o + m], -float("inf")))
-                top = torch.topk(conf, k).indices
-                tok[i, lo + top] = torch.where(masked[top], x0[o:o + m][top], tok[i, lo + top])
-            o += m
+        sampler(hidden, seqs, tok)                   # K8 + K9: unmask in place on the device
         for s in seqs:
             s.advance()
     torch.cuda.synchronize()
@@ -455,6 +431,96 @@ def bench_rope(dev, n=8 * 384, Hq=32, Hkv=32, D=128, theta=500000.0):
                 torch_expr_us=ms_torch * 1e3, speedup_vs_torch_expr=ms_torch / ms)
 
 
+def reference_style_unmask(x0, x0_p, tok, wins, mask_id):
+    """The reference's per-sequence unmasking loop (model_runner.py:895-949)
+    in torch ops, for timing beside K9: mask test, .item() of the mask count,
+    topk and the index write-back per sequence."""
+    import math
+
+    r = 0
+    for b, (lo, n, sr) in enumerate(wins):
+        t = tok[b]
+        mask_index = t[lo:lo + n] == mask_id
+        confidence = torch.where(mask_index, x0_p[r:r + n], -float("inf"))
+        nmask = mask_index.sum().item()
+        k = min(math.ceil(float(nmask) / sr), nmask)
+        top = torch.topk(confidence, k=k).indices
+        t[lo + top] = x0[r:r + n][top]
+        r += n
+
+
+def bench_sampler(dev):
+    """K8 + K9 at the C2 shapes (LLaDA vocabulary 126464): the dense step's
+    8 x 128 generated rows and the block step's 8 x 32, vs torch's
+    softmax + max on the same logits and the reference's per-sequence loop;
+    plus the whole sampling step (LM head GEMM included) at 8 x 128."""
+    from dllm_serve_amd import _capi
+    from dllm_serve_amd.engine.sampler import RemaskSampler
+    from dllm_serve_amd.engine.sequence import Sequence
+
+    V, mask_id = 126464, 126336
+    out = {}
+    for name, B, n in (("dense_8x128_rows", 8, 128), ("block_8x32_rows", 8, 32)):
+        M = B * n
+        g = torch.Generator(device=dev).manual_seed(M)
+        # distinct logits buffers, 0.5 GB in all (beyond the 256 MB last-level cache)
+        nb = max(2, (512 << 20) // (2 * M * V))
+        bufs = [(torch.randn(M, V, generator=g, device=dev) * 1.3).to(torch.bfloat16) for _ in range(nb)]
+        x0 = torch.empty(M, dtype=torch.int64, device=dev)
+        p = torch.empty(M, dtype=torch.bfloat16, device=dev)
+        ws = torch.empty(_capi.softmax_max_workspace_size(M, V), dtype=torch.uint8, device=dev)
+        state = {"i": 0}
+
+        def k8():
+            _capi.softmax_max(bufs[state["i"] % nb], x0, p, ws)
+            state["i"] += 1
+
+        ms8 = time_kernel(k8, iters=20 * nb)
+        ms_t = time_kernel(lambda: torch.max(torch.softmax(bufs[0], dim=-1), dim=-1), iters=10)
+        # K9 over 8 windows of n positions, most of them masked; steps_remain
+        # large so that each call unmasks one position per sequence
+        N = 256 + n
+        tok = torch.full((B, N), mask_id, dtype=torch.int64, device=dev)
+        params = torch.tensor([(b * N + 256, n, b * n, 10 ** 6, 0) for b in range(B)], dtype=torch.int32,
+                              device=dev)
+        ms9 = time_kernel(lambda: _capi.lowconf_unmask(tok, params, B, n, x0, p, mask_id), iters=40)
+        tok.fill_(mask_id)
+        wins = [(256, n, 10 ** 6)] * B
+
+        def ref_loop():
+            reference_style_unmask(x0, p, tok, wins, mask_id)
+
+        ms_loop = time_kernel(ref_loop, iters=10, warmup=2)
+        algo = 2.0 * M * V
+        out[name] = dict(rows=M, k8_us=ms8 * 1e3, k8_gbs=algo / (ms8 * 1e-3) / 1e9,
+                         k8_frac_of_hbm=algo / (ms8 * 1e-3) / 1e9 / PEAK_HBM_GBS,
+                         torch_softmax_max_us=ms_t * 1e3, k8_speedup_vs_torch=ms_t / ms8,
+                         k9_us=ms9 * 1e3, reference_loop_us=ms_loop * 1e3, k9_speedup_vs_loop=ms_loop / ms9)
+        del bufs
+    # whole sampling step of the C2 dense batch: hidden [8 x 384, 4096], LM head [126464, 4096]
+    g = torch.Generator(device=dev).manual_seed(7)
+    H = 4096
+    w = (torch.randn(V, H, generator=g, device=dev, dtype=torch.bfloat16) * 0.02)
+    hidden = torch.randn(8 * 384, H, generator=g, device=dev, dtype=torch.bfloat16)
+    seqs = [Sequence([1] * 256, 128, mask_id, None, device=dev, steps=128) for _ in range(8)]
+    tok = torch.tensor([s.token_ids for s in seqs], dtype=torch.int64, device=dev)
+    sampler = RemaskSampler(lambda h: h @ w.t(), mask_id)
+    ms_step = time_kernel(lambda: sampler(hidden, seqs, tok), iters=10, warmup=2)
+
+    def ref_step():
+        sel = torch.cat([hidden[b * 384 + 256:(b + 1) * 384] for b in range(8)])
+        pr, xx = torch.max(torch.softmax(sel @ w.t(), dim=-1), dim=-1)
+        reference_style_unmask(xx, pr, tok, [(256, 128, 128)] * 8, mask_id)
+
+    ms_ref = time_kernel(ref_step, iters=10, warmup=2)
+    ms_gemm = time_kernel(lambda: hidden[:1024] @ w.t(), iters=10)
+    out["c2_dense_sampling_step"] = dict(ms=ms_step, reference_style_ms=ms_ref, lm_head_gemm_ms=ms_gemm,
+                                         speedup=ms_ref / ms_step)
+    del w, hidden
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(lens, Hq, Hkv, D, budget_s=12.0):
     """Oracle (numpy fp32) attention of the headline step's layer calls on the
     host cores; bounded sample of whole layer calls."""
@@ -507,9 +573,19 @@ def profile_run(lens, Hq, Hkv, D, n_layers, dev):
     c5["store"]()
     for _ in range(4):
         c5["attend"]()
+    del c5
+    # K8 softmax-max over the C2 dense step's 8 x 128 rows of LLaDA logits, two buffers alternating
+    V, M = 126464, 1024
+    g = torch.Generator(device=dev).manual_seed(M)
+    bufs = [(torch.randn(M, V, generator=g, device=dev) * 1.3).to(torch.bfloat16) for _ in range(2)]
+    x0 = torch.empty(M, dtype=torch.int64, device=dev)
+    p = torch.empty(M, dtype=torch.bfloat16, device=dev)
+    ws = torch.empty(_capi.softmax_max_workspace_size(M, V), dtype=torch.uint8, device=dev)
+    for i in range(8):
+        _capi.softmax_max(bufs[i % 2], x0, p, ws)
     torch.cuda.synchronize()
     log(f"profile run done: 3 x 256 MiB copies, {n_layers} attention launches, {n_layers} RoPE launches "
-        f"({n} tokens), 1 C5 store + 4 C5 block-cached launches")
+        f"({n} tokens), 1 C5 store + 4 C5 block-cached launches, 8 K8 launches ({M} x {V} logits)")
 
 
 TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "attn_dense_kernel_llada_c2_8x384_counters.md")
@@ -538,8 +614,9 @@ def main() -> None:
     ap.add_argument("--quick", action="store_true", help="headline only (no extra shapes, no CPU baseline)")
     ap.add_argument("--profile", action="store_true",
                     help="counter run: a 256 MiB device copy (x3, calibrates FETCH_SIZE / WRITE_SIZE), 32 "
-                         "launches of the headline attention kernel, 32 RoPE launches, the C5 store and 4 C5 "
-                         "block-cached launches; prints no JSON")
+                         "launches of the headline attention kernel, 32 RoPE launches, the C5 store, 4 C5 "
+                         "block-cached launches and 8 softmax-max launches over 1024 x 126464 logits; "
+                         "prints no JSON")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); this build has no multi-GPU path",
@@ -581,6 +658,9 @@ def main() -> None:
         extra["hbm_copy_1gib"] = {k: round(v, 1) for k, v in bench_copy(dev).items()}
         log("K7: RoPE of q and k at the C2 step's token count")
         extra["rope_c2_tokens"] = {k: round(v, 3) for k, v in bench_rope(dev).items()}
+        log("K8 / K9: remask sampler at the C2 shapes")
+        extra["sampler_c2"] = {k: ({kk: round(vv, 3) for kk, vv in v.items()} if isinstance(v, dict) else v)
+                               for k, v in bench_sampler(dev).items()}
         log("C4: sparse vs dense attention per 64-step block")
         r4s = bench_sparse_c4(dev)
         extra["c4_head_sparse_per_block"] = {k: round(v, 3) for k, v in r4s.items()}

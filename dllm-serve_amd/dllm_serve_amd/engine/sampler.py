@@ -27,21 +27,34 @@ from .. import _capi
 MAX_WINDOW = 8192  # SamplingParams caps gen_length at 8192 (sampling_params.py:18-22)
 
 
+def _total_steps(seq) -> int:
+    sp = getattr(seq, "sampling_params", None)
+    return sp.steps if sp is not None else seq.steps
+
+
 def step_windows(seqs) -> list[tuple[int, int, int, int, int]]:
     """(hidden row of the window's first position, window start position,
     window length, steps_remain, first-token rule) per sequence, for the rows
-    the runner fed this step (Sequence.step_rows, packed in order)."""
+    the runner fed this step, packed in sequence order: only the current
+    block in the reuse-cache state, every position otherwise
+    (model_runner.py:240-256).  Reads only what the reference's Sequence and
+    PerRequestSparseState expose (num_prompt_tokens, num_tokens,
+    current_step, sampling_params.steps, compute_block_boundaries,
+    step_in_block, the state properties)."""
     out, row0 = [], 0
     for seq in seqs:
-        start, n_fed = seq.step_rows()
         st = seq.sparse_state
+        P, N = seq.num_prompt_tokens, seq.num_tokens
         if st is None:                                    # :797-802, :911-912
-            lo, hi = seq.num_prompt_tokens, seq.num_tokens
-            steps_remain = seq.steps - seq.current_step
+            start, n_fed = 0, N
+            lo, hi = P, N
+            steps_remain = _total_steps(seq) - seq.current_step
             first = 0
         else:                                             # :803-818, :913-915
-            lo, n = st.block_span(seq.num_prompt_tokens, seq.num_tokens)
+            lo, n = st.compute_block_boundaries(P, N)
+            n = max(0, n)
             hi = lo + n
+            start, n_fed = (lo, n) if st.should_reuse_cache else (0, N)
             steps_remain = n - st.step_in_block
             first = int(st.is_full_attention and n > 0)   # :920
         if steps_remain == 0:

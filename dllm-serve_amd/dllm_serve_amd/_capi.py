@@ -55,6 +55,8 @@ SIGNATURES = {
     "dllm_softmax_max_workspace_size": (_SZ, [_I, _I]),
     "dllm_softmax_max": (_I, [_P, _I64, _I, _I, _P, _P, _P, _SZ, _P]),
     "dllm_lowconf_unmask": (_I, [_P, _I64, _P, _I, _I, _P, _P, _I64, _I64, _P, _P]),
+    "dllm_step_build": (_I, [_P, _P, _P, _P, _I, _I64, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _P, _P, _I, _P, _P]),
+    "dllm_step_advance": (_I, [_P, _I, _P]),
 }
 
 _lib = None
@@ -227,3 +229,25 @@ def lowconf_unmask(tokens, seq_params, n_seq, max_win, x0, conf, mask_id, n_unma
                                  x0.data_ptr(), conf.data_ptr(), x0.numel(), int(mask_id), _ptr(n_unmasked),
                                  _stream(tokens.device))
     _check(rc, "dllm_lowconf_unmask")
+
+
+def step_build(state, ratio, pages, page_off, n_seq, tok_stride, cu, dense_ids, cached_ids, slot_off, jobs,
+               slots, positions, token_index, smp_params, smp_rows, counts):
+    """S1: one step's launch tables, fed-row positions and sampler windows
+    from the device state table (see include/dllm_attn.h)."""
+    _require_gpu(state, ratio, page_off, cu, counts)
+    lib = load()
+    rc = lib.dllm_step_build(state.data_ptr(), ratio.data_ptr(), _ptr(pages), page_off.data_ptr(), n_seq,
+                             int(tok_stride), cu.data_ptr(), dense_ids.data_ptr(), cached_ids.data_ptr(),
+                             slot_off.data_ptr(), jobs.data_ptr(), _ptr(slots), slots.numel(),
+                             positions.data_ptr(), token_index.data_ptr(), positions.numel(),
+                             smp_params.data_ptr(), smp_rows.data_ptr(), smp_rows.numel(), counts.data_ptr(),
+                             _stream(state.device))
+    _check(rc, "dllm_step_build")
+
+
+def step_advance(state, n_seq):
+    """S2: advance every sequence's step / block / cache state on the device."""
+    _require_gpu(state)
+    rc = load().dllm_step_advance(state.data_ptr(), n_seq, _stream(state.device))
+    _check(rc, "dllm_step_advance")

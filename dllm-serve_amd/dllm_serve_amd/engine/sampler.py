@@ -146,6 +146,19 @@ class RemaskSampler:
         return n_unmasked
 
 
+def sample_device_windows(sampler: "RemaskSampler", hidden_states: torch.Tensor, tokens: torch.Tensor,
+                          smp_rows: torch.Tensor, smp_params: torch.Tensor, max_win: int) -> torch.Tensor:
+    """The sampling step with windows built on the device (dllm_step_build's
+    smp_rows / smp_params): nothing is computed or copied on the host."""
+    n_seq = smp_params.shape[0]
+    n_unmasked = torch.zeros(n_seq, dtype=torch.int32, device=hidden_states.device)
+    if smp_rows.numel() == 0:
+        return n_unmasked
+    x0, x0_p = sampler.logits_max(hidden_states.index_select(0, smp_rows))
+    _capi.lowconf_unmask(tokens.view(-1), smp_params, n_seq, max_win, x0, x0_p, sampler.mask_token_id, n_unmasked)
+    return n_unmasked
+
+
 def token_lists(tokens: torch.Tensor, seqs, token_offsets: Optional[Seq[int]] = None) -> list[list[int]]:
     """The reference's return value (one token list per sequence); one copy to the host."""
     host = tokens.cpu()

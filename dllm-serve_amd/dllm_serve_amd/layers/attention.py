@@ -79,17 +79,15 @@ def load_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor, 
     _capi.load_kvcache(key, value, k_cache, v_cache, slot, N, D)
 
 
-class StepPlan:
-    """Launch tables of one diffusion forward (shared by all layers).
+class StepLayout:
+    """Host integers of one diffusion step: per-sequence mode (0 full, 1 full
+    + select-and-store, 2 block vs cache, -1 unrecognised), fed rows, block
+    span and n_keep, and the launch sizes derived from them (attention.py:
+    168-265, sequence.py:99-152).  No tensors are created."""
 
-    Built from host integers of ``context.seqs``; uploaded with one copy.
-    """
-
-    def __init__(self, context, device: torch.device, num_kv_heads: int, head_dim: int, num_heads: int):
-        seqs = context.seqs
+    def __init__(self, seqs):
         if not seqs:
             raise ValueError("diffusion context has no sequences")
-        self.device = device
         rows, modes, spans, keeps = [], [], [], []
         for seq in seqs:
             st = seq.sparse_state
@@ -124,17 +122,58 @@ class StepPlan:
                 rows.append(N)
                 spans.append((0, 0))
                 keeps.append(0)
+        self.modes, self.rows, self.spans, self.keeps = modes, rows, spans, keeps
         self.n_seq = len(seqs)
         self.total_rows = int(sum(rows))
-        cu = np.zeros(self.n_seq + 1, dtype=np.int64)
-        cu[1:] = np.cumsum(rows)
+        self.cu = np.zeros(self.n_seq + 1, dtype=np.int64)
+        self.cu[1:] = np.cumsum(rows)
         self.any_skipped = any(m == -1 for m in modes)
+        self.dense = [i for i, m in enumerate(modes) if m in (0, 1)]
+        self.jobs_idx = [i for i, m in enumerate(modes) if m == 1]
+        self.cached = [i for i, m in enumerate(modes) if m == 2]
+        self.n_dense = len(self.dense)
+        self.max_q_dense = max((rows[i] for i in self.dense), default=0)
+        self.n_job = len(self.jobs_idx)
+        self.max_kc = max((rows[i] - spans[i][1] for i in self.jobs_idx), default=0)
+        self.max_keep = max((keeps[i] for i in self.jobs_idx), default=0)
+        self.max_blk = max((spans[i][1] for i in self.jobs_idx), default=0)
+        self.n_cached = len(self.cached)
+        self.max_q_cached = max((rows[i] for i in self.cached), default=0)
+        self.max_keys_cached = max((rows[i] + keeps[i] for i in self.cached), default=0)
+        self.total_slots = sum(keeps[i] for i in self.cached + self.jobs_idx)
+        self.head_select = None
+        self.pool_k = None
+        for i in self.jobs_idx:
+            cfg = seqs[i].sparse_state.config
+            hs, pk = bool(cfg.head_select), int(cfg.pool_kernel)
+            if self.head_select is None:
+                self.head_select, self.pool_k = hs, pk
+            elif (hs, pk) != (self.head_select, self.pool_k):
+                raise NotImplementedError("sequences with different head_select / pool_kernel in one step")
 
-        dense = [i for i, m in enumerate(modes) if m in (0, 1)]
-        jobs_idx = [i for i, m in enumerate(modes) if m == 1]
-        cached = [i for i, m in enumerate(modes) if m == 2]
-        self.n_dense = len(dense)
-        self.max_q_dense = max((rows[i] for i in dense), default=0)
+    def signature(self) -> tuple:
+        """Everything a captured step's launches depend on."""
+        return (tuple(self.modes), tuple(self.rows), tuple(self.keeps), tuple(s[1] for s in self.spans),
+                self.head_select, self.pool_k)
+
+
+class StepPlan:
+    """Launch tables of one diffusion forward (shared by all layers).
+
+    ``StepPlan(context, device, ...)`` builds them from host integers of
+    ``context.seqs`` and uploads them with one asynchronous copy;
+    ``StepPlan.from_device`` wraps tables the device-side builder wrote."""
+
+    _SCALARS = ("n_seq", "total_rows", "any_skipped", "n_dense", "max_q_dense", "n_job", "max_kc", "max_keep",
+                "max_blk", "n_cached", "max_q_cached", "max_keys_cached", "head_select", "pool_k")
+
+    def __init__(self, context, device: torch.device, num_kv_heads: int = 0, head_dim: int = 0, num_heads: int = 0,
+                 layout: StepLayout | None = None):
+        seqs = context.seqs
+        lay = layout if layout is not None else StepLayout(seqs)
+        self._take(lay, device)
+        rows, spans, keeps, cu = lay.rows, lay.spans, lay.keeps, lay.cu
+        dense, jobs_idx, cached = lay.dense, lay.jobs_idx, lay.cached
 
         # slots of sparse sequences: state-2 sequences first (contiguous, so
         # slot_off below brackets each of them), then state-1 sequences
@@ -155,31 +194,26 @@ class StepPlan:
         self.slots = torch.cat(slot_parts) if slot_parts else torch.zeros(1, dtype=torch.int32, device=device)
 
         # selection jobs: row0, n_tok, blk_start, blk_len, n_keep, slot_off
-        self.n_job = len(jobs_idx)
         jobs = np.zeros((max(1, self.n_job), 6), dtype=np.int64)
         for r, i in enumerate(jobs_idx):
             bs, bl = spans[i]
             jobs[r] = (cu[i], rows[i], bs, bl, keeps[i], slot_base[i])
-        self.max_kc = max((rows[i] - spans[i][1] for i in jobs_idx), default=0)
-        self.max_keep = max((keeps[i] for i in jobs_idx), default=0)
-        self.max_blk = max((spans[i][1] for i in jobs_idx), default=0)
 
         # cached (state 2) segments: slot offsets indexed by position in `cached`
-        self.n_cached = len(cached)
         slot_off = np.zeros(self.n_cached + 1, dtype=np.int64)
         for r, i in enumerate(cached):
             slot_off[r] = slot_base[i]
             slot_off[r + 1] = slot_base[i] + keeps[i]
-        self.max_q_cached = max((rows[i] for i in cached), default=0)
-        self.max_keys_cached = max((rows[i] + keeps[i] for i in cached), default=0)
 
-        # one host->device copy of every int32 table
+        # one asynchronous host->device copy (from pinned memory) of every int32 table
         parts = [cu, np.array(dense or [0]), np.array(cached or [0]), slot_off, jobs.reshape(-1)]
         flat = np.concatenate([p.astype(np.int64) for p in parts])
         if flat.size and (flat.max() >= 2**31 or flat.min() < -(2**31)):
             raise ValueError("step tables exceed int32")
         host = torch.from_numpy(flat.astype(np.int32))
-        dev = host.to(device, non_blocking=False)
+        if device.type == "cuda":
+            host = host.pin_memory()
+        dev = host.to(device, non_blocking=True)
         o = 0
         self.cu = dev[o:o + cu.size]; o += cu.size
         self.dense_ids = dev[o:o + max(1, len(dense))]; o += max(1, len(dense))
@@ -187,18 +221,21 @@ class StepPlan:
         self.slot_off = dev[o:o + slot_off.size]; o += slot_off.size
         self.jobs = dev[o:o + jobs.size]
 
-        self.head_select = None
-        self.pool_k = None
-        for i in jobs_idx:
-            cfg = seqs[i].sparse_state.config
-            hs, pk = bool(cfg.head_select), int(cfg.pool_kernel)
-            if self.head_select is None:
-                self.head_select, self.pool_k = hs, pk
-            elif (hs, pk) != (self.head_select, self.pool_k):
-                raise NotImplementedError("sequences with different head_select / pool_kernel in one step")
-
+    def _take(self, lay: StepLayout, device) -> None:
+        self.device = device
+        for k in self._SCALARS:
+            setattr(self, k, getattr(lay, k))
         self._ws = {}
         self.last_idx = None
+
+    @classmethod
+    def from_device(cls, lay: StepLayout, device, cu, dense_ids, cached_ids, slot_off, jobs, slots) -> "StepPlan":
+        """Plan over tables already on the device (written by dllm_step_build)."""
+        self = cls.__new__(cls)
+        self._take(lay, device)
+        self.cu, self.dense_ids, self.cached_ids = cu, dense_ids, cached_ids
+        self.slot_off, self.jobs, self.slots = slot_off, jobs, slots
+        return self
 
     def workspace(self, key: str, nbytes: int) -> torch.Tensor | None:
         if nbytes <= 0:

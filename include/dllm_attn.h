@@ -232,6 +232,54 @@ int dllm_lowconf_unmask(int64_t* tokens, int64_t n_tokens, const int32_t* seq_pa
                         const int64_t* x0, const dllm_bf16* conf, int64_t n_rows, int64_t mask_id,
                         int32_t* n_unmasked, void* stream);
 
+/*
+ * S1 -- device-side step metadata.  Replaces the host loops that build one
+ * diffusion step's inputs and launch tables: ModelRunner._run_diffusion's
+ * row / position / slot-list construction (dllmserve/engine/model_runner.py:
+ * 231-321, slot lists :257-273,287-302), the per-sequence mode and
+ * selection sizes of _mixed_sparse_dense_attention (dllmserve/layers/
+ * attention.py:168-265, sequence.py:99-152) and the sampler's windows
+ * (model_runner.py:791-818,911-920).
+ *
+ * seq_state is int32 [n_seq][10] per sequence: {P (prompt tokens), N (all
+ * tokens), sparse (0: no SparseConfig), block_len, current_block_idx,
+ * step_in_block, cache_state, delay_step, steps, current_step}; ratio is the
+ * f64 retention ratio per sequence.  Sequence b's cache pages are
+ * pages[page_off[b] .. page_off[b+1]).  Outputs, for the step the state
+ * describes (n = n_seq):
+ *   cu [n+1]            packed row offsets of the fed rows (all N rows; only
+ *                       the block's rows in cache state 2)
+ *   dense_ids [max(1,n)]  sequences of full attention (state 0/1 or none), in order
+ *   cached_ids [max(1,n)] sequences in state 2, in order
+ *   slot_off [n+1]      their slot ranges in `slots`
+ *   jobs [max(1,n)][6]  state-1 selection jobs {row0, n_tok, blk_start,
+ *                       blk_len, n_keep, slot_off} (as dllm_select_kv_store)
+ *   slots [slots_cap]   n_keep slots per state-2 sequence, then per state-1
+ *                       sequence: page[r / 256] * 256 + r % 256 (-1 past its pages)
+ *   positions, token_index [rows_cap] (int64) position of each fed row and
+ *                       its index b * tok_stride + position in the token table
+ *   smp_params [n][5], smp_rows [win_cap]  the dllm_lowconf_unmask parameters
+ *                       and the fed row of each window position
+ *   counts [8]          {rows, n_dense, n_cached, n_job, slots, window
+ *                       positions, capacity exceeded (0/1), sequences in an
+ *                       invalid state}
+ * n_keep = min(max(1, int(Kc * ratio)), Kc).  When a capacity is exceeded only
+ * the per-sequence tables are written.  n_seq must be at most 1024.
+ */
+int dllm_step_build(const int32_t* seq_state, const double* ratio, const int32_t* pages, const int32_t* page_off,
+                    int n_seq, int64_t tok_stride, int32_t* cu, int32_t* dense_ids, int32_t* cached_ids,
+                    int32_t* slot_off, int32_t* jobs, int32_t* slots, int slots_cap, int64_t* positions,
+                    int64_t* token_index, int rows_cap, int32_t* smp_params, int64_t* smp_rows, int win_cap,
+                    int32_t* counts, void* stream);
+
+/*
+ * S2 -- advance every sequence's state by one denoising step on the device:
+ * current_step += 1 (Scheduler.postprocess, scheduler.py:117-120) and, for
+ * sparse sequences, PerRequestSparseState.advance_step (state.py:77-104).
+ * block_len must be >= 1.
+ */
+int dllm_step_advance(int32_t* seq_state, int n_seq, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

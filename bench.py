@@ -321,14 +321,20 @@ class LLaDA8B:
         return self._rms(h, self.ln_f)
 
 
-def denoise(model, batch, prompt, gen, steps, block, sparse, dev, seed=0, ratio=1.0, head_select=True):
-    """Generate `gen` tokens for `batch` random prompts; returns (seconds, steps).
+def denoise(model, batch, prompt, gen, steps, block, sparse, dev, seed=0, ratio=1.0, head_select=True,
+            graphed=False):
+    """Generate `gen` tokens for `batch` random prompts; returns (seconds,
+    steps, final token table).
 
     Token ids stay on the device; each step's LM head runs on the rows that
     may be unmasked (all generated rows when dense, the current block when
     cached) and RemaskSampler unmasks ceil(masked / remaining steps) of them
-    by confidence = max softmax probability (K8 + K9, no host round trip)."""
-    from dllm_serve_amd.engine.sampler import RemaskSampler
+    by confidence = max softmax probability (K8 + K9, no host round trip).
+    graphed=True builds each step's tables on the device (dllm_step_build /
+    dllm_step_advance) and replays the steps from HIP graphs captured once
+    per launch shape (StepGraphs; the captures run inside the timed loop)."""
+    from dllm_serve_amd.engine.device_step import DeviceStepState, StepGraphs
+    from dllm_serve_amd.engine.sampler import RemaskSampler, sample_device_windows
     from dllm_serve_amd.engine.sequence import PageAllocator, Sequence, prepare_step
     from dllm_serve_amd.sparse.state import SparseConfig
     from dllm_serve_amd.utils.context import reset_context
@@ -347,31 +353,52 @@ def denoise(model, batch, prompt, gen, steps, block, sparse, dev, seed=0, ratio=
             alloc.allocate(s)
     tok = torch.tensor([s.token_ids for s in seqs], dtype=torch.int64, device=dev)  # [B, N]
     sampler = RemaskSampler(lambda h: h @ model.lm_head.t(), c["mask_id"])
+    graphs = None
+    if graphed:
+        def step_fn(t):
+            hidden = model.forward(tok.view(-1).index_select(0, t.token_index), t.positions)
+            sample_device_windows(sampler, hidden, tok, t.smp_rows, t.smp_params, t.max_win)
+
+        graphs = StepGraphs(DeviceStepState(seqs, dev, tok.stride(0)), step_fn)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
-        rows = [s.step_rows() for s in seqs]
-        ids = torch.cat([tok[i, a:a + n] for i, (a, n) in enumerate(rows)])
-        pos = torch.cat([torch.arange(a, a + n, device=dev) for a, n in rows])
-        prepare_step(seqs, dev, build_inputs=False)  # Context: cu_seqlens, slot lists, seqs
-        hidden = model.forward(ids, pos)
-        reset_context()
-        sampler(hidden, seqs, tok)                   # K8 + K9: unmask in place on the device
+        if graphs is not None:
+            graphs.run(seqs)
+        else:
+            rows = [s.step_rows() for s in seqs]
+            ids = torch.cat([tok[i, a:a + n] for i, (a, n) in enumerate(rows)])
+            pos = torch.cat([torch.arange(a, a + n, device=dev) for a, n in rows])
+            prepare_step(seqs, dev, build_inputs=False)  # Context: cu_seqlens, slot lists, seqs
+            hidden = model.forward(ids, pos)
+            reset_context()
+            sampler(hidden, seqs, tok)                   # K8 + K9: unmask in place on the device
         for s in seqs:
             s.advance()
     torch.cuda.synchronize()
-    return time.perf_counter() - t0, steps
+    secs = time.perf_counter() - t0
+    del graphs
+    return secs, steps, tok
 
 
 def bench_denoise(dev):
-    """C2: LLaDA-8B, B=8, prompt 256, gen 128, steps 128, block 32."""
+    """C2: LLaDA-8B, B=8, prompt 256, gen 128, steps 128, block 32; eager
+    steps on host-built tables, and the same run replayed from HIP graphs
+    over device-built tables (its tokens must equal the eager run's)."""
     model = LLaDA8B(dev)
     out = {}
     for name, sparse in (("cached_ret1", True), ("dense", False)):
         denoise(model, 8, 256, 128, 4, 32, sparse, dev, seed=1)  # warm-up (kernels, allocator)
-        secs, steps = denoise(model, 8, 256, 128, 128, 32, sparse, dev)
+        secs, steps, tok = denoise(model, 8, 256, 128, 128, 32, sparse, dev)
         out[name] = dict(seconds=round(secs, 3), steps=steps, tokens_per_s=round(8 * 128 / secs, 1),
                          ms_per_step=round(secs / steps * 1e3, 3))
+        secs_g, _, tok_g = denoise(model, 8, 256, 128, 128, 32, sparse, dev, graphed=True)
+        out[name + "_graphs"] = dict(seconds=round(secs_g, 3), steps=steps,
+                                     tokens_per_s=round(8 * 128 / secs_g, 1),
+                                     ms_per_step=round(secs_g / steps * 1e3, 3),
+                                     tokens_equal_eager=bool(torch.equal(tok, tok_g)))
+        del tok, tok_g
+        torch.cuda.empty_cache()
     del model
     torch.cuda.empty_cache()
     return out
@@ -384,7 +411,7 @@ def bench_denoise_c4(dev):
     out = {}
     for name, sparse in (("head_sparse_r0.5", True), ("dense", False)):
         denoise(model, 4, 1024, 256, 3, 64, sparse, dev, seed=1, ratio=0.5)  # warm-up
-        secs, steps = denoise(model, 4, 1024, 256, 64, 64, sparse, dev, ratio=0.5)
+        secs, steps, _ = denoise(model, 4, 1024, 256, 64, 64, sparse, dev, ratio=0.5)
         out[name] = dict(seconds=round(secs, 3), steps=steps, tokens_per_s=round(4 * 64 / secs, 1),
                          ms_per_step=round(secs / steps * 1e3, 3))
     out["speedup"] = round(out["dense"]["seconds"] / out["head_sparse_r0.5"]["seconds"], 2)

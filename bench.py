@@ -704,7 +704,7 @@ def main() -> None:
     # The binding ceiling of the headline kernel: HBM when its arithmetic
     # intensity (algorithmic FLOPs / algorithmic bytes) is below the machine
     # balance peak_flops / peak_bw, else MFMA.
-    kernel_name = "attn_dense_kernel<4, 1, 2, 32, 3>"
+    kernel_name = "attn_dense_kernel<12, 1, 2, 32, 3>"
     intensity = r["flops_per_call"] / r["bytes_per_call"]
     balance = PEAK_BF16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)
     mfma_frac = r["tflops_kernel"] / PEAK_BF16_TFLOPS

@@ -327,9 +327,11 @@ template <int NW, int NQ, int ST, int TK, int OCC>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void attn_dense_kernel(AttnArgs a) {
   constexpr int BM = 32 * NW * NQ;
   constexpr int STAGE = 2 * TK * 256;                      // K + V tile bytes
-  constexpr int DMA_PER_WAVE = TK * 256 / 1024 / NW;       // 1 KiB DMA instructions per wave, K (same for V)
-  constexpr int DMA_TILE = 2 * DMA_PER_WAVE;               // this wave's DMA instructions per tile
-  static_assert(DMA_PER_WAVE >= 1 && TK % 32 == 0, "tile shape");
+  constexpr int NDMA = TK * 256 / 1024;                    // 1 KiB DMA instructions per matrix per tile
+  constexpr int DMA_PER_WAVE = (NDMA + NW - 1) / NW;       // per wave (waves >= NDMA issue none when NW > NDMA)
+  constexpr int DMA_TILE = 2 * DMA_PER_WAVE;               // this wave's DMA instructions per tile, K and V
+  static_assert(TK % 32 == 0, "tile shape");
+  static_assert(NDMA % NW == 0 || (NW > NDMA && ST == 2), "an uneven DMA split needs the full wait of two stages");
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int L = xcd_remap(blockIdx.x, gridDim.x);
   if (L >= a.logical_blocks) return;
@@ -362,11 +364,13 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(OCC, OC
   DenseAddr ad;
   dense_addr(ad, lane, kS, vS);
 
-  // DMA instruction j (global index q = DMA_PER_WAVE*wave + j) covers tile rows 4q..4q+3.
+  // DMA instruction j (global index q = DMA_PER_WAVE*wave + j, or q = wave
+  // when there are more wavefronts than instructions) covers tile rows 4q..4q+3.
   auto issue = [&](uint8_t* stage, int k0) {
 #pragma unroll
     for (int j = 0; j < DMA_PER_WAVE; ++j) {
-      const int q = DMA_PER_WAVE * wave + j;
+      const int q = NW > NDMA ? wave : DMA_PER_WAVE * wave + j;
+      if (q >= NDMA) break;  // wave-uniform
       const uint32_t row = (uint32_t)(k0 + 4 * q);
       dma16(krs, stage + q * 1024, row * kS + (ad.kdma ^ (uint32_t)(64 * (q & 3))));
       dma16(vrs, stage + TK * 256 + q * 1024, row * vS + ad.vdma);
@@ -438,7 +442,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(OCC, OC
     // The wave's 32 rows x 256 bytes land in its own 8 KiB of the (now free)
     // K/V stages, chunks XOR-swizzled by row; read back, instruction j
     // carries rows 4j .. 4j+3, one 16-byte chunk per lane.
-    static_assert(NW * 8192 <= ST * STAGE, "O staging fits in the K/V stages");
+    // O staging needs NW * 8 KiB: the launch gives max(ST * STAGE, NW * 8192) bytes of LDS
     const float l_tot = pair_sum32(st.l_run[0]);
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
     __syncthreads();  // every wavefront is done reading the K/V stages
@@ -890,7 +894,12 @@ extern "C" int dllm_attn_varlen_fwd(const dllm_bf16* q, const dllm_bf16* k, cons
   a.q_stride = q_stride_tok; a.k_stride = k_stride_tok; a.v_stride = v_stride_tok; a.o_stride = o_stride_tok;
   a.n_seg = n_seg; a.Hkv = Hkv; a.g = Hq / Hkv;
   const bool wide = max_seqlen_k >= DENSE_LONG_K;
-  const int nw = wide ? 8 : 4;
+  // (segment, KV head) pairs of 257..384 M rows: one 12-wavefront workgroup
+  // each, so the pair's K/V tiles are read into LDS once instead of by three
+  // workgroups (3 % faster for 8 x 384 tokens, 32 heads).
+  const int64_t m_rows = (int64_t)max_seqlen_q * (Hq / Hkv);
+  const bool one_wg = !wide && m_rows > 256 && m_rows <= 384;
+  const int nw = wide ? 8 : (one_wg ? 12 : 4);
   const int bm = 32 * nw;
   a.mtiles = (int)(((int64_t)max_seqlen_q * a.g + bm - 1) / bm);
   a.n_split = 1;
@@ -901,11 +910,14 @@ extern "C" int dllm_attn_varlen_fwd(const dllm_bf16* q, const dllm_bf16* k, cons
   // Long key streams: 8 wavefronts (256 M rows) per workgroup, 64-key tiles,
   // one workgroup per CU.  Shorter ones: 4 wavefronts, 32-key tiles, three
   // workgroups per CU (independent workgroups overlap the softmax of one with
-  // the MFMAs of another).  Measured: the 4-wavefront shape is 5-12 % faster
-  // up to 1280 keys (8 x 384, 4 x 1280, Dream GQA varlen with up to 1245
-  // keys), the 8-wavefront one 6 % faster at 4096 keys.
-  auto kern = wide ? attn_dense_kernel<8, 1, DENSE_ST, 64, 2> : attn_dense_kernel<4, 1, DENSE_ST, 32, 3>;
-  const int lds_bytes = DENSE_ST * 2 * (wide ? 64 : 32) * 256;
+  // the MFMAs of another), or 12 wavefronts for pairs of 257..384 M rows.
+  // Measured: the 4-wavefront shape is 5-12 % faster up to 1280 keys
+  // (4 x 1280, Dream GQA varlen with up to 1245 keys), the 8-wavefront one
+  // 6 % faster at 4096 keys.
+  auto kern = wide ? attn_dense_kernel<8, 1, DENSE_ST, 64, 2>
+                   : (one_wg ? attn_dense_kernel<12, 1, DENSE_ST, 32, 3> : attn_dense_kernel<4, 1, DENSE_ST, 32, 3>);
+  int lds_bytes = DENSE_ST * 2 * (wide ? 64 : 32) * 256;
+  if (nw * 8192 > lds_bytes) lds_bytes = nw * 8192;  // O staging
   if ((rc = set_lds(kern, lds_bytes, name))) return rc;
   const int nb = (int)((logical + 7) / 8 * 8);
   kern<<<dim3(nb), dim3(64 * nw), lds_bytes, reinterpret_cast<hipStream_t>(stream)>>>(a);

@@ -46,6 +46,8 @@ def test_c1_single_layer(dev):
     ([200, 517, 1], 28, 4),                            # Dream GQA, g = 7
     ([96, 160], 8, 2),                                 # g = 4
     ([1000], 4, 4),
+    ([300, 384, 1, 257, 383], 16, 16),               # 257..384 M rows: one 12-wavefront workgroup per pair
+    ([64, 96, 7], 16, 4),                              # the same launch with GQA (96 x 4 = 384 M rows)
 ])
 def test_varlen_ragged(dev, lens, Hq, Hkv):
     print(f"varlen lens={lens} Hq={Hq} Hkv={Hkv}", flush=True)

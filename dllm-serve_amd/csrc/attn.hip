@@ -252,8 +252,8 @@ __device__ __forceinline__ void dense_tile(const uint8_t* Ks, const uint8_t* Vs,
   // chains that interleave instead of one chain waiting on itself.
   // Each S^T block's head-dim reduction is split over SPLIT partial
   // accumulators (kk % SPLIT) so KB*NQ*SPLIT independent MFMA chains are in
-  // flight: a dependent 32x32x16 MFMA waits several issue slots for its
-  // predecessor, and two chains per wavefront leave the matrix pipe idle.
+  // flight: a dependent 32x32x16 MFMA waits for its predecessor, and a
+  // single chain per wavefront leaves the matrix pipe idle.
   // 64-key tiles already give two independent S^T chains (one per 32-key
   // block), so their reduction is not split (1.5-2 % faster at 2 x 4096).
   constexpr int SPLIT = TK == 32 ? kSSplit : 1;

@@ -27,3 +27,41 @@ def test_select_fixtures():
         qb, kb, idx = mg.select_case(Lb, Kc, Hq, Hkv, n_keep, hs, pk, seed)
         assert np.array_equal(qb, fx[f"{name}_q"]) and np.array_equal(kb, fx[f"{name}_k"])
         assert np.array_equal(idx, fx[f"{name}_idx"]), name
+
+
+def test_rope_fixture():
+    import torch
+
+    from oracle import rope as orope
+
+    fx = np.load(os.path.join(HERE, "rope_cases.npz"))
+    n = fx["x"].shape[0]
+    # the oracle on the stored table rows (row i of table_rows is position pos[i])
+    got = orope.rotate_table(bf16_bits_to_f32(fx["x"]), np.arange(n), fx["table_rows"])
+    assert np.array_equal(got, fx["out"])
+    # the table rows are the ones the reference's construction gives
+    now = mg.rope_case()
+    assert np.allclose(now["table_rows"], fx["table_rows"], rtol=0, atol=2e-7)
+    # torch's f32 expression on the same rows (the reference's own ops)
+    x = torch.from_numpy(bf16_bits_to_f32(fx["x"]))
+    cs = torch.from_numpy(fx["table_rows"])[:, None, :]
+    x1, x2 = torch.chunk(x, 2, dim=-1)
+    y = torch.cat((x1 * cs[..., :64] - x2 * cs[..., 64:], x2 * cs[..., :64] + x1 * cs[..., 64:]), -1)
+    assert np.array_equal(y.to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16), fx["out"])
+
+
+def test_sampler_fixture():
+    import torch
+
+    from oracle import sampler as osm
+
+    fx = np.load(os.path.join(HERE, "sampler_cases.npz"))
+    x0, p = osm.softmax_max(fx["logits"])
+    assert np.array_equal(x0, fx["x0"]) and np.array_equal(p, fx["x0_p"])
+    t = torch.from_numpy(fx["logits"].view(np.int16)).view(torch.bfloat16)
+    tp, ti = torch.max(torch.softmax(t, dim=-1), dim=-1)       # the reference's ops on the CPU
+    assert np.array_equal(ti.numpy(), fx["x0"])
+    assert np.all(np.abs(tp.view(torch.int16).numpy().view(np.uint16).astype(int) - fx["x0_p"].astype(int)) <= 1)
+    assert fx["x0"][35] == 3 and fx["x0"][36] == 40 and fx["x0"][37] == 0 and fx["x0"][39] == 4095
+    out, nun = osm.unmask_step(fx["tokens"], fx["params"], fx["pred"], fx["conf"], int(fx["mask_id"]))
+    assert np.array_equal(out, fx["tokens_out"]) and np.array_equal(nun, fx["n_unmasked"])

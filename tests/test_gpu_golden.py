@@ -53,3 +53,41 @@ def test_select_fixtures(dev):
         torch.cuda.synchronize()
         want = fx[f"{name}_idx"] if hs else fx[f"{name}_idx"][None, :]
         assert np.array_equal(idx.cpu().numpy()[0], want), name
+
+
+def test_rope_fixture(dev):
+    print("golden rope", flush=True)
+    fx = np.load(os.path.join(HERE, "rope_cases.npz"))
+    n, H, D = fx["x"].shape
+    table = torch.zeros(int(fx["max_position"]), D, dtype=torch.float32)
+    pos = torch.from_numpy(fx["pos"])
+    table[pos] = torch.from_numpy(fx["table_rows"])
+    x = torch.from_numpy(fx["x"].view(np.int16)).view(torch.bfloat16).to(dev)
+    out = torch.empty_like(x)
+    k = torch.empty(n, 0, D, dtype=torch.bfloat16, device=dev)
+    _capi.rope_neox(x, out, k, k, pos.to(dev), table.to(dev), n, H, 0, D)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().view(torch.int16).numpy().view(np.uint16), fx["out"])
+
+
+def test_sampler_fixture(dev):
+    print("golden sampler", flush=True)
+    fx = np.load(os.path.join(HERE, "sampler_cases.npz"))
+    logits = torch.from_numpy(fx["logits"].view(np.int16)).view(torch.bfloat16).to(dev)
+    M, V = logits.shape
+    x0 = torch.empty(M, dtype=torch.int64, device=dev)
+    p = torch.empty(M, dtype=torch.bfloat16, device=dev)
+    ws = torch.empty(_capi.softmax_max_workspace_size(M, V), dtype=torch.uint8, device=dev)
+    _capi.softmax_max(logits, x0, p, ws)
+    tok = torch.from_numpy(fx["tokens"]).to(dev)
+    params = torch.from_numpy(fx["params"]).to(dev)
+    conf = torch.from_numpy(fx["conf"].view(np.int16)).view(torch.bfloat16).to(dev)
+    pred = torch.from_numpy(fx["pred"]).to(dev)
+    nun = torch.empty(params.shape[0], dtype=torch.int32, device=dev)
+    _capi.lowconf_unmask(tok, params, params.shape[0], int(fx["params"][:, 1].max()), pred, conf,
+                         int(fx["mask_id"]), nun)
+    torch.cuda.synchronize()
+    assert np.array_equal(x0.cpu().numpy(), fx["x0"])
+    d = np.abs(p.cpu().view(torch.int16).numpy().view(np.uint16).astype(int) - fx["x0_p"].astype(int))
+    assert d.max() <= 1 and np.mean(d == 0) >= 0.9
+    assert np.array_equal(tok.cpu().numpy(), fx["tokens_out"]) and np.array_equal(nun.cpu().numpy(), fx["n_unmasked"])

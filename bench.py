@@ -503,6 +503,21 @@ def bench_sampler(dev):
             state["i"] += 1
 
         ms8 = time_kernel(k8, iters=20 * nb)
+        temp1 = torch.ones(M, dtype=torch.float64, device=dev)
+
+        def k8_gumbel():
+            _capi.softmax_max_sample(bufs[state["i"] % nb], temp1, 1234 + state["i"], 0, x0, p, ws)
+            state["i"] += 1
+
+        ms8g = time_kernel(k8_gumbel, iters=4 * nb)
+
+        def ref_gumbel():  # add_gumbel_noise + softmax + max as the reference runs them (f64 tensors)
+            lg = bufs[0].to(torch.float64)
+            noise = torch.rand_like(lg)
+            v = (lg.exp() / (-torch.log(noise))).to(torch.bfloat16)
+            torch.max(torch.softmax(v, dim=-1), dim=-1)
+
+        ms_tg = time_kernel(ref_gumbel, iters=3, warmup=1)
         ms_t = time_kernel(lambda: torch.max(torch.softmax(bufs[0], dim=-1), dim=-1), iters=10)
         # K9 over 8 windows of n positions, most of them masked; steps_remain
         # large so that each call unmasks one position per sequence
@@ -522,6 +537,8 @@ def bench_sampler(dev):
         out[name] = dict(rows=M, k8_us=ms8 * 1e3, k8_gbs=algo / (ms8 * 1e-3) / 1e9,
                          k8_frac_of_hbm=algo / (ms8 * 1e-3) / 1e9 / PEAK_HBM_GBS,
                          torch_softmax_max_us=ms_t * 1e3, k8_speedup_vs_torch=ms_t / ms8,
+                         k8_temperature1_us=ms8g * 1e3, torch_gumbel_softmax_max_us=ms_tg * 1e3,
+                         k8_temperature1_speedup_vs_torch=ms_tg / ms8g,
                          k9_us=ms9 * 1e3, reference_loop_us=ms_loop * 1e3, k9_speedup_vs_loop=ms_loop / ms9)
         del bufs
     # whole sampling step of the C2 dense batch: hidden [8 x 384, 4096], LM head [126464, 4096]

@@ -17,6 +17,14 @@
 // {m, s, first index of m}; the final kernel merges a row's records in one
 // wavefront.  HBM-bound: 2 V bytes per row, read once.
 //
+// With a per-row temperature T > 0 the row is first transformed as the
+// reference's add_gumbel_noise does (model_runner.py:592-600):
+//   v_j = bf16(exp(f64 l_j) / (-log u_j)^T),   u_j uniform in [0, 1) (f64)
+// and the softmax-max runs over v.  u_j comes from a counter-based generator
+// (SplitMix64 of seed + (c + 1) * 0x9E3779B97F4A7C15, c = (row_base + row) *
+// V + j, top 53 bits), so a row's draws do not depend on how rows are
+// grouped into launches; torch's own generator stream is not reproduced.
+//
 // K9 (lowconf_unmask_kernel) is the per-sequence unmasking step that follows
 // (model_runner.py:895-949): in the sequence's window of token positions,
 // count the masked ones, unmask k = min(ceil(nmask / steps_remain), nmask) of
@@ -65,15 +73,38 @@ __device__ __forceinline__ void smx_wave_reduce(float& m, float& s, int& i) {
   }
 }
 
+__device__ __forceinline__ uint64_t splitmix64_at(uint64_t seed, uint64_t c) {
+  uint64_t z = seed + (c + 1) * 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+// exp(l) / (-log u)^T in f64, rounded to f32 and then to bf16 (the value the
+// reference stores back into its bf16 logits), returned as f32.
+__device__ __forceinline__ float gumbel_value(float l, double T, uint64_t seed, uint64_t c) {
+  const double u = (double)(splitmix64_at(seed, c) >> 11) * 0x1.0p-53;
+  const double nl = -log(u);
+  const double g = T == 1.0 ? nl : pow(nl, T);
+  const double v = exp((double)l) / g;
+  return bf16_bits_to_f32(f32_to_bf16_bits((float)v));
+}
+
 // Fold 8 logits (one 16-byte chunk starting at column e0) into the running
 // (m, s, i).  A thread's chunks arrive in increasing column order, so a tie
 // with the running max keeps the earlier index.
-__device__ __forceinline__ void smx_chunk(u32x4_t v, int e0, float& m, float& s, int& i) {
+template <bool GUMBEL>
+__device__ __forceinline__ void smx_chunk(u32x4_t v, int e0, float& m, float& s, int& i, double T = 0.0,
+                                          uint64_t seed = 0, uint64_t c0 = 0) {
   float f[8];
 #pragma unroll
   for (int w = 0; w < 4; ++w) {
     f[2 * w] = __uint_as_float(v[w] << 16);
     f[2 * w + 1] = __uint_as_float(v[w] & 0xffff0000u);
+  }
+  if (GUMBEL) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) f[k] = gumbel_value(f[k], T, seed, c0 + (uint64_t)k);
   }
   const float cm = fmaxf(fmaxf(fmaxf(f[0], f[1]), fmaxf(f[2], f[3])), fmaxf(fmaxf(f[4], f[5]), fmaxf(f[6], f[7])));
   if (cm > m) {
@@ -104,8 +135,12 @@ struct SmxArgs {
   SmxRec* part;     // [M][S]
   int64_t* x0;
   uint16_t* x0p;
+  const double* temp;  // per-row temperature (nullable: no transform)
+  uint64_t seed;
+  int64_t row_base;
 };
 
+template <bool GUMBEL>
 __global__ __launch_bounds__(kSmxThreads) void smx_partial_kernel(SmxArgs a) {
   __shared__ float red_m[kSmxThreads / 64];
   __shared__ float red_s[kSmxThreads / 64];
@@ -125,8 +160,21 @@ __global__ __launch_bounds__(kSmxThreads) void smx_partial_kernel(SmxArgs a) {
       const int cc = c + u * kSmxThreads;
       v[u] = cc < c1 ? ld128_stream(base + 8 * (int64_t)cc) : ninf;
     }
+    if (!GUMBEL) {
 #pragma unroll
-    for (int u = 0; u < 4; ++u) smx_chunk(v[u], 8 * (c + u * kSmxThreads), m, s, idx);
+      for (int u = 0; u < 4; ++u) smx_chunk<false>(v[u], 8 * (c + u * kSmxThreads), m, s, idx);
+    } else {
+      const double T = a.temp[row];
+      const uint64_t rc = (uint64_t)(a.row_base + row) * (uint64_t)a.V;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int e0 = 8 * (c + u * kSmxThreads);
+        if (T > 0.0 && c + u * kSmxThreads < c1)  // padding chunks stay -inf
+          smx_chunk<true>(v[u], e0, m, s, idx, T, a.seed, rc + (uint64_t)e0);
+        else
+          smx_chunk<false>(v[u], e0, m, s, idx);
+      }
+    }
   }
   smx_wave_reduce(m, s, idx);
   const int wave = threadIdx.x >> 6;
@@ -168,12 +216,15 @@ __global__ __launch_bounds__(256) void smx_final_kernel(SmxArgs a) {
     const float thr = m - 0.015625f;
     int found = INT_MAX;
     const int nch = (idx + 7) >> 3;
+    const double T = a.temp ? a.temp[row] : 0.0;
+    const uint64_t rc = (uint64_t)(a.row_base + row) * (uint64_t)a.V;
     for (int c = lane; c < nch; c += 64) {
       const u32x4_t v = ld128(base + 8 * (int64_t)c);
 #pragma unroll
       for (int k = 7; k >= 0; --k) {
         const uint32_t w = v[k >> 1];
-        const float f = (k & 1) ? __uint_as_float(w & 0xffff0000u) : __uint_as_float(w << 16);
+        float f = (k & 1) ? __uint_as_float(w & 0xffff0000u) : __uint_as_float(w << 16);
+        if (T > 0.0) f = gumbel_value(f, T, a.seed, rc + (uint64_t)(8 * c + k));
         const int j = 8 * c + k;
         if (j < idx && f >= thr && f32_to_bf16_bits(expf(f - m) / s) == P) found = min(found, j);
       }
@@ -288,9 +339,9 @@ extern "C" size_t dllm_softmax_max_workspace_size(int M, int V) {
   return (size_t)M * S * sizeof(SmxRec);
 }
 
-extern "C" int dllm_softmax_max(const uint16_t* logits, int64_t ld, int M, int V, int64_t* x0, uint16_t* x0_p,
-                                void* workspace, size_t workspace_bytes, void* stream) {
-  static const char* name = "dllm_softmax_max";
+static int softmax_max_launch(const char* name, const uint16_t* logits, int64_t ld, int M, int V,
+                              const double* row_temperature, uint64_t seed, int64_t row_base, int64_t* x0,
+                              uint16_t* x0_p, void* workspace, size_t workspace_bytes, void* stream) {
   if (M < 0 || V < 0) return fail(DLLM_ERR_INVALID_ARG, "%s: negative size", name);
   if (M == 0) return DLLM_OK;
   if (V == 0 || V % 8 != 0)
@@ -317,12 +368,32 @@ extern "C" int dllm_softmax_max(const uint16_t* logits, int64_t ld, int M, int V
   a.part = reinterpret_cast<SmxRec*>(workspace);
   a.x0 = x0;
   a.x0p = x0_p;
+  a.temp = row_temperature;
+  a.seed = seed;
+  a.row_base = row_base;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  smx_partial_kernel<<<dim3((unsigned)(M * S)), dim3(kSmxThreads), 0, st>>>(a);
+  if (row_temperature)
+    smx_partial_kernel<true><<<dim3((unsigned)(M * S)), dim3(kSmxThreads), 0, st>>>(a);
+  else
+    smx_partial_kernel<false><<<dim3((unsigned)(M * S)), dim3(kSmxThreads), 0, st>>>(a);
   int rc = check_launch(name);
   if (rc != DLLM_OK) return rc;
   smx_final_kernel<<<dim3((unsigned)((M + 3) / 4)), dim3(256), 0, st>>>(a);
   return check_launch(name);
+}
+
+extern "C" int dllm_softmax_max(const uint16_t* logits, int64_t ld, int M, int V, int64_t* x0, uint16_t* x0_p,
+                                void* workspace, size_t workspace_bytes, void* stream) {
+  return softmax_max_launch("dllm_softmax_max", logits, ld, M, V, nullptr, 0, 0, x0, x0_p, workspace,
+                            workspace_bytes, stream);
+}
+
+extern "C" int dllm_softmax_max_sample(const uint16_t* logits, int64_t ld, int M, int V,
+                                       const double* row_temperature, uint64_t seed, int64_t row_base, int64_t* x0,
+                                       uint16_t* x0_p, void* workspace, size_t workspace_bytes, void* stream) {
+  if (row_base < 0) return fail(DLLM_ERR_INVALID_ARG, "dllm_softmax_max_sample: negative row_base");
+  return softmax_max_launch("dllm_softmax_max_sample", logits, ld, M, V, row_temperature, seed, row_base, x0, x0_p,
+                            workspace, workspace_bytes, stream);
 }
 
 extern "C" int dllm_lowconf_unmask(int64_t* tokens, int64_t n_tokens, const int32_t* seq_params, int n_seq,

@@ -54,6 +54,7 @@ SIGNATURES = {
     "dllm_rope_neox": (_I, [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _P, _I64, _I, _I, _I, _I, _P]),
     "dllm_softmax_max_workspace_size": (_SZ, [_I, _I]),
     "dllm_softmax_max": (_I, [_P, _I64, _I, _I, _P, _P, _P, _SZ, _P]),
+    "dllm_softmax_max_sample": (_I, [_P, _I64, _I, _I, _P, ctypes.c_uint64, _I64, _P, _P, _P, _SZ, _P]),
     "dllm_lowconf_unmask": (_I, [_P, _I64, _P, _I, _I, _P, _P, _I64, _I64, _P, _P]),
     "dllm_step_build": (_I, [_P, _P, _P, _P, _I, _I64, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _P, _P, _I, _P, _P]),
     "dllm_step_advance": (_I, [_P, _I, _P]),
@@ -218,6 +219,19 @@ def softmax_max(logits, x0, x0_p, workspace):
     rc = lib.dllm_softmax_max(logits.data_ptr(), logits.stride(0), M, V, x0.data_ptr(), x0_p.data_ptr(),
                               workspace.data_ptr(), ws_bytes, _stream(logits.device))
     _check(rc, "dllm_softmax_max")
+
+
+def softmax_max_sample(logits, row_temperature, seed, row_base, x0, x0_p, workspace):
+    """K8 with Gumbel noise on the rows whose temperature is > 0
+    (row_temperature: float64 [M] on the device, or None)."""
+    _require_gpu(logits, row_temperature, x0, x0_p, workspace)
+    lib = load()
+    M, V = logits.shape
+    ws_bytes = workspace.numel() * workspace.element_size()
+    rc = lib.dllm_softmax_max_sample(logits.data_ptr(), logits.stride(0), M, V, _ptr(row_temperature),
+                                     int(seed) & 0xFFFFFFFFFFFFFFFF, int(row_base), x0.data_ptr(), x0_p.data_ptr(),
+                                     workspace.data_ptr(), ws_bytes, _stream(logits.device))
+    _check(rc, "dllm_softmax_max_sample")
 
 
 def lowconf_unmask(tokens, seq_params, n_seq, max_win, x0, conf, mask_id, n_unmasked=None):

@@ -76,10 +76,12 @@ class RemaskSampler:
     ``token_offsets[b]`` giving sequence b's first token."""
 
     def __init__(self, compute_logits: Callable[[torch.Tensor], torch.Tensor], mask_token_id: int,
-                 max_logprobs: Optional[int] = None):
+                 max_logprobs: Optional[int] = None, seed: int = 0):
         self.compute_logits = compute_logits
         self.mask_token_id = int(mask_token_id)
         self.max_logprobs = max_logprobs  # rows per LM-head chunk (None: all at once)
+        self.seed = int(seed)             # base of the per-call noise seeds (temperature > 0)
+        self.calls = 0
         self._ws = None
 
     def _workspace(self, M: int, V: int, device) -> torch.Tensor:
@@ -88,8 +90,10 @@ class RemaskSampler:
             self._ws = torch.empty(max(need, 16), dtype=torch.uint8, device=device)
         return self._ws
 
-    def logits_max(self, rows: torch.Tensor):
-        """x0 (int64) and x0_p (bf16) of the gathered hidden rows."""
+    def logits_max(self, rows: torch.Tensor, row_temperature: Optional[torch.Tensor] = None, seed: int = 0):
+        """x0 (int64) and x0_p (bf16) of the gathered hidden rows; rows whose
+        row_temperature (float64, device) is > 0 are sampled with Gumbel noise
+        drawn from (seed, row index)."""
         M = rows.shape[0]
         dev = rows.device
         x0 = torch.empty(M, dtype=torch.int64, device=dev)
@@ -100,16 +104,27 @@ class RemaskSampler:
             logits = self.compute_logits(rows[a:b])
             if logits.dtype != torch.bfloat16 or logits.dim() != 2 or logits.stride(-1) != 1:
                 raise ValueError("compute_logits must return [rows, vocab] bf16 with a contiguous last dim")
-            _capi.softmax_max(logits, x0[a:b], x0_p[a:b], self._workspace(b - a, logits.shape[1], dev))
+            ws = self._workspace(b - a, logits.shape[1], dev)
+            if row_temperature is None:
+                _capi.softmax_max(logits, x0[a:b], x0_p[a:b], ws)
+            else:
+                _capi.softmax_max_sample(logits, row_temperature[a:b], seed, a, x0[a:b], x0_p[a:b], ws)
         return x0, x0_p
 
     def __call__(self, hidden_states: torch.Tensor, seqs: Seq, tokens: torch.Tensor,
                  token_offsets: Optional[Seq[int]] = None, remasking: str = "low_confidence",
                  temperature: float = 0.0, generator: Optional[torch.Generator] = None) -> torch.Tensor:
         """Unmask this step's tokens in place; returns the per-sequence count
-        of unmasked positions (int32 [B], on the device)."""
-        if temperature > 0:
-            raise NotImplementedError("Gumbel-noise sampling (temperature > 0) is not built; use temperature 0")
+        of unmasked positions (int32 [B], on the device).
+
+        Temperatures come from each sequence's ``sampling_params`` when it
+        has them, else from ``temperature`` (one value or one per sequence).
+        Rows of a sequence with temperature > 0 get the reference's Gumbel
+        noise (add_gumbel_noise, model_runner.py:592-600) with draws from a
+        counter-based generator seeded by (seed, call number).  Every such
+        sequence gets its noise; the reference's v2 path applies it only to
+        the first sequence of each logits chunk (its cu_seqlens there is the
+        cumsum of one length, model_runner.py:826-836,859-866)."""
         if remasking not in ("low_confidence", "random"):
             raise NotImplementedError(remasking)               # :908-909
         _capi._require_gpu(hidden_states, tokens)
@@ -125,19 +140,34 @@ class RemaskSampler:
             if token_offsets is None or len(token_offsets) != len(seqs):
                 raise ValueError("a flat token store needs token_offsets, one per sequence")
             offs = [int(o) for o in token_offsets]
-        params, idx, r = [], [], 0
+        temps = []
+        for b, seq in enumerate(seqs):
+            sp = getattr(seq, "sampling_params", None)
+            if sp is not None:
+                temps.append(float(sp.temperature))
+            elif isinstance(temperature, (list, tuple)):
+                temps.append(float(temperature[b]))
+            else:
+                temps.append(float(temperature))
+        params, idx, row_t, r = [], [], [], 0
         for b, (h0, lo, n, sr, first) in enumerate(win):
             if n > MAX_WINDOW:
                 raise ValueError(f"window of {n} positions exceeds {MAX_WINDOW}")
             params.append((offs[b] + lo, n, r, sr, first))
             idx.append(torch.arange(h0, h0 + n, dtype=torch.int64))
+            row_t.append(torch.full((n,), max(0.0, temps[b]), dtype=torch.float64))
             r += n
         n_unmasked = torch.zeros(len(seqs), dtype=torch.int32, device=dev)
         if r == 0:
             return n_unmasked
         sel = torch.cat(idx).pin_memory().to(dev, non_blocking=True)
         p = torch.tensor(params, dtype=torch.int32).pin_memory().to(dev, non_blocking=True)
-        x0, x0_p = self.logits_max(hidden_states.index_select(0, sel))
+        rt = None
+        if any(t > 0 for t in temps):
+            rt = torch.cat(row_t).pin_memory().to(dev, non_blocking=True)
+        seed = (self.seed * 0x9E3779B97F4A7C15 + self.calls) & 0xFFFFFFFFFFFFFFFF
+        self.calls += 1
+        x0, x0_p = self.logits_max(hidden_states.index_select(0, sel), rt, seed)
         conf = x0_p
         if remasking == "random":                              # :903-905
             conf = torch.rand(r, device=dev, generator=generator).to(torch.bfloat16)

@@ -206,6 +206,24 @@ int dllm_softmax_max(const dllm_bf16* logits, int64_t ld, int M, int V, int64_t*
                      void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * K8 with sampling noise.  Replaces add_gumbel_noise + softmax + max for
+ * sequences sampled at temperature > 0 (dllmserve/engine/model_runner.py:
+ * 592-600,826-836,859-866).  Row r with row_temperature[r] = T > 0 is first
+ * transformed as the reference does:
+ *   v_j = bf16(f32(exp(f64 l_j) / (-log u_j)^T)),  u_j uniform in [0, 1) (f64)
+ * and x0 / x0_p are then taken over v as in dllm_softmax_max; rows with
+ * T <= 0 are plain.  u_j = 2^-53 * (SplitMix64(seed + (c + 1) *
+ * 0x9E3779B97F4A7C15) >> 11) with c = (row_base + r) * V + j: counter-based,
+ * so the draws of a row depend on (seed, row_base + r, j) only, not on how
+ * rows are split into calls.  (torch's generator stream is not reproduced;
+ * the noise follows the same distribution.)  row_temperature may be null
+ * (then this is dllm_softmax_max).
+ */
+int dllm_softmax_max_sample(const dllm_bf16* logits, int64_t ld, int M, int V, const double* row_temperature,
+                            uint64_t seed, int64_t row_base, int64_t* x0, dllm_bf16* x0_p,
+                            void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * K9 -- low-confidence unmasking of one denoising step.  Replaces the
  * per-sequence loop of _reconstruct_and_sample_optimized_v2
  * (dllmserve/engine/model_runner.py:895-949: mask test, steps_remain,

@@ -6,6 +6,9 @@ Restates dllmserve/engine/model_runner.py:756-949
 (_reconstruct_and_sample_optimized_v2, temperature 0):
   softmax_max   probs = F.softmax(bf16 logits, -1) (f32 inside, bf16 out);
                 x0_p, x0 = torch.max(probs, -1)                     (:862-863, :886-887)
+  softmax_max_sample  the same after add_gumbel_noise (:592-600) on rows of
+                temperature > 0, with the counter-based SplitMix64 draws the
+                K8 kernel uses
   unmask_step   per sequence: mask test over the window, steps_remain,
                 num_to_unmask = min(ceil(nmask / steps_remain), nmask), the
                 is_full_attention first-token rule, torch.topk over the
@@ -18,7 +21,9 @@ from __future__ import annotations
 
 import numpy as np
 
-from .bf16 import bf16_bits_to_f32, f32_to_bf16_bits
+from .bf16 import bf16_bits_to_f32, f32_to_bf16_bits, f64_to_bf16_bits
+
+GAMMA = 0x9E3779B97F4A7C15
 
 
 def softmax_max(logit_bits: np.ndarray, s_scale: float = 1.0) -> tuple[np.ndarray, np.ndarray]:
@@ -37,6 +42,47 @@ def softmax_max(logit_bits: np.ndarray, s_scale: float = 1.0) -> tuple[np.ndarra
     pv = bf16_bits_to_f32(p)
     x0 = pv.argmax(axis=1).astype(np.int64)  # first maximal index
     return x0, p[np.arange(p.shape[0]), x0]
+
+
+def splitmix64_at(seed: int, c: np.ndarray) -> np.ndarray:
+    """SplitMix64 output for counters c (Steele, Lea & Flood 2014): mix of
+    seed + (c + 1) * golden gamma, with wrap-around uint64 arithmetic."""
+    c = np.asarray(c, dtype=np.uint64)
+    with np.errstate(over="ignore"):
+        z = np.uint64(seed & 0xFFFFFFFFFFFFFFFF) + (c + np.uint64(1)) * np.uint64(GAMMA)
+        z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+        z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+    return z ^ (z >> np.uint64(31))
+
+
+def uniforms(seed: int, row: int, V: int) -> np.ndarray:
+    """The f64 draws u_j in [0, 1) of logits row `row` (global index)."""
+    c = np.uint64(row) * np.uint64(V) + np.arange(V, dtype=np.uint64)
+    return (splitmix64_at(seed, c) >> np.uint64(11)).astype(np.float64) * 2.0 ** -53
+
+
+def gumbel_transform(logit_bits: np.ndarray, T: float, u: np.ndarray) -> np.ndarray:
+    """add_gumbel_noise (model_runner.py:592-600) on one bf16 row, stored
+    back as bf16 (f64 -> f32 -> bf16, the conversion of the bf16 assignment
+    at :833-835 / :864-866)."""
+    l = bf16_bits_to_f32(np.asarray(logit_bits, dtype=np.uint16)).astype(np.float64)
+    with np.errstate(divide="ignore"):
+        nl = -np.log(u)
+    g = nl if T == 1.0 else np.power(nl, T)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        v = np.exp(l) / g
+    return f64_to_bf16_bits(v)
+
+
+def softmax_max_sample(logit_bits: np.ndarray, row_temperature, seed: int, row_base: int = 0):
+    """softmax_max after the Gumbel transform of every row whose temperature
+    is > 0 (draws from `uniforms(seed, row_base + r, V)`)."""
+    b = np.array(logit_bits, dtype=np.uint16, copy=True).reshape(-1, np.asarray(logit_bits).shape[-1])
+    V = b.shape[1]
+    for r, T in enumerate(np.asarray(row_temperature, dtype=np.float64)):
+        if T > 0:
+            b[r] = gumbel_transform(b[r], float(T), uniforms(seed, row_base + r, V))
+    return softmax_max(b)
 
 
 def conf_order(bits: np.ndarray) -> np.ndarray:

@@ -147,4 +147,4 @@ def test_sampler_refuses_cpu_tensors():
     with pytest.raises(RuntimeError, match="GPU only"):
         s(torch.zeros(32, 8, dtype=torch.bfloat16), seqs, torch.zeros(2, 18, dtype=torch.int64))
     with pytest.raises(NotImplementedError):
-        s(torch.zeros(32, 8, dtype=torch.bfloat16), seqs, torch.zeros(2, 18, dtype=torch.int64), temperature=1.0)
+        s(torch.zeros(32, 8, dtype=torch.bfloat16), seqs, torch.zeros(2, 18, dtype=torch.int64), remasking="topk")

@@ -164,3 +164,47 @@ def test_unmask_first_token_rule():
     t2[0] = 5                                        # first position already known
     out, nun = osm.unmask_step(t2, [(0, n, 0, 4, 1)], x0, conf, MASK)      # nmask 7, k = 2
     assert nun[0] == 2 and out[0] == 5 and out[6] == 106 and out[7] == 107
+
+
+def test_splitmix64_known_answers():
+    # first outputs of SplitMix64 seeded with 0 (the published reference sequence)
+    got = [int(x) for x in osm.splitmix64_at(0, np.arange(3, dtype=np.uint64))]
+    assert got == [0xE220A8397B1DCDAF, 0x6E789E6AA1B965F4, 0x06C45D188009454F]
+    u = osm.uniforms(1234, 5, 100000)
+    assert u.min() >= 0.0 and u.max() < 1.0 and abs(u.mean() - 0.5) < 0.005
+    # a row's draws depend on its global index only
+    assert np.array_equal(osm.uniforms(7, 3, 64), osm.uniforms(7, 3, 64))
+    assert not np.array_equal(osm.uniforms(7, 3, 64), osm.uniforms(7, 4, 64))
+
+
+@pytest.mark.parametrize("T", [1.0, 0.5, 2.0])
+def test_gumbel_transform_matches_the_reference_ops(T):
+    """add_gumbel_noise's torch ops (model_runner.py:592-600) on the same draws,
+    stored back into a bf16 tensor as the reference's slice assignment does."""
+    rng = np.random.default_rng(int(T * 10))
+    V = 4096
+    bits = _bits(rng.standard_normal(V) * 3)
+    u = osm.uniforms(99, 2, V)
+    got = osm.gumbel_transform(bits, T, u)
+    lg = torch.from_numpy(bf16_bits_to_f32(bits)).to(torch.float64)
+    noise = torch.from_numpy(u)
+    want = lg.exp() / (-torch.log(noise)) ** T
+    dst = torch.empty(V, dtype=torch.bfloat16)
+    dst[:] = want
+    assert np.array_equal(got, dst.view(torch.int16).numpy().view(np.uint16))
+
+
+def test_gumbel_sampling_follows_softmax():
+    """Gumbel-max: at T = 1 the sampled index is distributed as softmax(l)."""
+    V, n = 8, 40000
+    l = np.log(np.array([1, 2, 3, 4, 6, 8, 12, 16], np.float64))
+    bits = np.tile(_bits(l.astype(np.float32)), (n, 1))
+    x0, p = osm.softmax_max_sample(bits, np.ones(n), seed=2024)
+    freq = np.bincount(x0, minlength=V) / n
+    want = np.exp(bf16_bits_to_f32(bits[0]).astype(np.float64))
+    want /= want.sum()
+    assert np.abs(freq - want).max() < 0.01, (freq, want)
+    # temperature 0 rows are plain softmax-max
+    x0b, pb = osm.softmax_max_sample(bits[:4], np.zeros(4), seed=1)
+    xa, pa = osm.softmax_max(bits[:4])
+    assert np.array_equal(x0b, xa) and np.array_equal(pb, pa)

@@ -4,7 +4,7 @@ A numpy restatement of what dLLM-Serve's attention hot path computes
 (dllmserve/layers/attention.py, sparse/state.py, engine/sequence.py,
 engine/model_runner.py:152-321, layers/rotary_embedding.py).  Only tests/,
 __graft_entry__.smoke() and bench.py's cpu_baseline leg may import it, and
-only as the checker; the product path (dllm-serve_amd/) never does.
+only to compute expected results; the product path (dllm-serve_amd/) never does.
 
 Modules
   bf16       bf16 <-> f32 bit conversions (round to nearest even)
@@ -13,7 +13,9 @@ Modules
   select     head / token KV selection with the explicit rounding and
              tie-break rule the GPU kernels implement
   kvcache    store_kvcache / load_kvcache by slot
-  rope       NeoX rotary embedding (input preparation; checker of the K7 kernel)
+  rope       NeoX rotary embedding (input preparation; expected results of the K7 kernel)
+  sampler    low-confidence remasking: softmax-max of logit rows (with the
+             Gumbel transform at temperature > 0) and the unmasking step
   configs    seeded synthetic inputs of the benchmark configurations
 
 Parity pins (what checks each function; see tests/test_oracle_*.py):
@@ -25,6 +27,11 @@ Parity pins (what checks each function; see tests/test_oracle_*.py):
   rope       norm preservation, relative-position invariance, position 0,
              quarter-turn / half-turn tables (exact swaps and negations),
              agreement with the torch f32 expression
+  sampler    torch's CPU softmax + max on the same bf16 rows, closed forms,
+             planted exact and rounding ties; torch.topk on tie-free
+             confidences, counting and tie-order invariants; the published
+             SplitMix64 outputs, the reference's add_gumbel_noise ops on the
+             same draws, Gumbel-max frequencies against softmax
 The reference's own tests hold no numeric fixtures for this path, and its
 package cannot be imported here (it needs flash_attn), so no function is
 pinned against reference-produced vectors.

@@ -3,7 +3,7 @@
 inv_freq[i] = 1 / base**(2i/D) (f32), angle = pos * inv_freq, cos/sin in f32;
 with x = [x1 | x2] split in halves:  y1 = x1 cos - x2 sin,  y2 = x2 cos + x1 sin.
 Computed in f32 like the reference.  ``apply`` prepares inputs (C1);
-``rotate_table`` is the checker of the K7 kernel: the reference's table
+``rotate_table`` gives the expected results of the K7 kernel: the reference's table
 lookup (rotary_embedding.py:47-49) and its f32 expression evaluated op by op
 (each product, sum and difference rounded to f32; :12-16), rounded to bf16.
 """

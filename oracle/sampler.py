@@ -1,6 +1,6 @@
 """Low-confidence remasking sampler (the step after the model's forward).
 
-TEST INFRASTRUCTURE ONLY: the checker of the K8 / K9 kernels.
+TEST INFRASTRUCTURE ONLY: expected results for the K8 / K9 kernels.
 
 Restates dllmserve/engine/model_runner.py:756-949
 (_reconstruct_and_sample_optimized_v2, temperature 0):

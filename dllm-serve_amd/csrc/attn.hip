@@ -31,7 +31,7 @@
 
 namespace dllm {
 
-constexpr int HD = 128;       // head dim handled by this build
+constexpr int HD = 128;       // the head dim these kernels handle
 
 struct AttnArgs {
   const uint16_t* q;
@@ -833,7 +833,7 @@ constexpr int DENSE_LONG_K = 2048;
 
 static int common_checks(const char* name, const void* q, const void* k, const void* v, const void* o, int Hq,
                          int Hkv, int D, int64_t qs, int64_t ks, int64_t vs, int64_t os) {
-  if (D != HD) return fail(DLLM_ERR_UNSUPPORTED, "%s: head_dim %d not supported (this build handles 128)", name, D);
+  if (D != HD) return fail(DLLM_ERR_UNSUPPORTED, "%s: head_dim %d not supported (the kernels handle 128)", name, D);
   if (Hq <= 0 || Hkv <= 0 || Hq % Hkv != 0)
     return fail(DLLM_ERR_INVALID_ARG, "%s: Hq=%d must be a positive multiple of Hkv=%d", name, Hq, Hkv);
   if (!q || !k || !v || !o) return fail(DLLM_ERR_INVALID_ARG, "%s: null tensor pointer", name);

@@ -15,7 +15,7 @@
 
 namespace dllm {
 
-constexpr int SHD = 128;         // head dim handled by this build
+constexpr int SHD = 128;         // the head dim these kernels handle
 constexpr int MAX_KC = 8192;     // candidates per sequence handled in LDS
 constexpr int TOPK_THREADS = 1024;
 
@@ -218,7 +218,7 @@ extern "C" int dllm_select_kv_store(const dllm_bf16* q, const dllm_bf16* k, cons
   const char* name = "dllm_select_kv_store";
   (void)max_blk;
   set_error("");
-  if (D != SHD) return fail(DLLM_ERR_UNSUPPORTED, "%s: head_dim %d not supported (this build handles 128)", name, D);
+  if (D != SHD) return fail(DLLM_ERR_UNSUPPORTED, "%s: head_dim %d not supported (the kernels handle 128)", name, D);
   if (Hq <= 0 || Hkv <= 0 || Hq % Hkv) return fail(DLLM_ERR_INVALID_ARG, "%s: Hq=%d / Hkv=%d", name, Hq, Hkv);
   if (n_job < 0 || max_kc < 0 || max_keep < 0) return fail(DLLM_ERR_INVALID_ARG, "%s: negative size", name);
   if (n_job == 0 || max_kc == 0 || max_keep == 0) return DLLM_OK;

@@ -31,7 +31,7 @@ typedef uint16_t dllm_bf16; /* bfloat16 bit pattern */
 
 #define DLLM_OK 0
 #define DLLM_ERR_INVALID_ARG (-1) /* shape / stride / alignment / size mismatch */
-#define DLLM_ERR_UNSUPPORTED (-2) /* valid request this build does not implement (e.g. head_dim != 128) */
+#define DLLM_ERR_UNSUPPORTED (-2) /* valid request the library does not implement (e.g. head_dim != 128) */
 #define DLLM_ERR_WORKSPACE (-3)   /* workspace pointer missing or too small */
 #define DLLM_ERR_HIP (-4)         /* a HIP runtime call or kernel launch failed */
 

@@ -136,6 +136,13 @@ def prepare_step(seqs: list[Sequence], device, block_size: int = 256, build_inpu
     Rows of a sequence are all its tokens for cache states 0/1 and only the
     current block for state 2; slot lists are given for states 1/2.
     """
+    dev = torch.device(device)
+    pinned = dev.type == "cuda"
+
+    def upload(t: torch.Tensor) -> torch.Tensor:
+        # asynchronous copies from pinned memory: building a step never waits for the GPU
+        return t.pin_memory().to(dev, non_blocking=True) if pinned else t.to(dev)
+
     ids, pos, lens, slot_mapping = [], [], [], []
     for seq in seqs:
         st = seq.sparse_state
@@ -147,12 +154,10 @@ def prepare_step(seqs: list[Sequence], device, block_size: int = 256, build_inpu
         if st is None or st.is_full_attention:
             slot_mapping.append([])
         else:
-            slot_mapping.append(
-                torch.tensor(slot_mapping_for(seq, block_size), dtype=torch.int32).to(device, non_blocking=True)
-            )
+            slot_mapping.append(upload(torch.tensor(slot_mapping_for(seq, block_size), dtype=torch.int32)))
     cu = torch.zeros(len(seqs) + 1, dtype=torch.int32)
     cu[1:] = torch.cumsum(torch.tensor(lens, dtype=torch.int32), 0)
-    cu = cu.to(device)
+    cu = upload(cu)
     set_context(True, cu_seqlens_q=None, cu_seqlens_k=cu, max_seqlen_q=0,
                 max_seqlen_k=int(sum(lens)), slot_mapping=slot_mapping, is_diffusion=True, seqs=seqs)
     if not build_inputs:

@@ -622,6 +622,74 @@ def cpu_baseline(lens, Hq, Hkv, D, budget_s=12.0):
                        f"numpy fp32 oracle, {dt:.1f} s, threads = BLAS default on {cores} host cores")
 
 
+def cpu_other_configs():
+    """The oracle (numpy fp32) on the other configurations' single layer calls,
+    on the host cores: C1 whole attention (1 x 512 tokens), C4 full step
+    (4 x 1280) and reuse step (4 x 64 rows against 608 cached + 64 block rows),
+    C5 (32 x 32 rows against 2048-4096 cached rows)."""
+    from oracle import attention as oatt
+    from oracle import configs
+
+    out = {}
+
+    def timed(fn, reps):
+        fn()
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return sorted(ts)[len(ts) // 2]
+
+    q, k, v, cu, scale = configs.c1_single_layer()
+    qn, kn, vn, cun = q.numpy(), k.numpy(), v.numpy(), cu.numpy()
+    t = timed(lambda: oatt.varlen(qn, kn, vn, cun, cun, scale, dtype=np.float32), 5)
+    fl = configs.attention_flops([512], [512], 32, 128)
+    out["c1_512_tokens"] = dict(seconds=round(t, 4), gflops=round(fl / t / 1e9, 1))
+    q, k, v, cu = configs.packed_qkv([1280] * 4, 32, 32, 128, seed=4, dtype=torch.float32)
+    qn, kn, vn, cun = q.numpy(), k.numpy(), v.numpy(), cu.numpy()
+    t = timed(lambda: oatt.varlen(qn, kn, vn, cun, cun, 128 ** -0.5, dtype=np.float32), 1)
+    fl = configs.attention_flops([1280] * 4, [1280] * 4, 32, 128)
+    out["c4_full_step_layer"] = dict(seconds=round(t, 3), gflops=round(fl / t / 1e9, 1))
+    rng = np.random.default_rng(0)
+    n_c, blk = 608, 64
+    kc = rng.standard_normal((4 * n_c, 32, 128)).astype(np.float32)
+    vc = rng.standard_normal((4 * n_c, 32, 128)).astype(np.float32)
+    qb = rng.standard_normal((4 * blk, 32, 128)).astype(np.float32)
+    slots = [list(range(i * n_c, (i + 1) * n_c)) for i in range(4)]
+
+    def reuse():
+        for i in range(4):
+            r = slice(i * blk, (i + 1) * blk)
+            oatt.block_cached(qb[r], qb[r], qb[r], kc, vc, slots[i], 128 ** -0.5, dtype=np.float32)
+
+    t = timed(reuse, 3)
+    fl = configs.attention_flops([blk] * 4, [n_c + blk] * 4, 32, 128)
+    by = configs.attention_bytes([blk] * 4, [n_c + blk] * 4, 32, 32, 128)
+    out["c4_reuse_step_layer"] = dict(seconds=round(t, 4), gflops=round(fl / t / 1e9, 1),
+                                      gbs_bf16_equivalent=round(by / t / 1e9, 2))
+    c = configs.c5_cached()
+    kp, vp = c["k_pre"].float().numpy(), c["v_pre"].float().numpy()
+    qc, kb, vb = c["q"].float().numpy(), c["k"].float().numpy(), c["v"].float().numpy()
+    off = np.cumsum([0] + c["prefix"])
+    slots5 = [list(range(off[i], off[i + 1])) for i in range(len(c["prefix"]))]  # prefixes packed in order
+
+    def c5():
+        for i in range(len(c["prefix"])):
+            r = slice(i * c["blk"], (i + 1) * c["blk"])
+            oatt.block_cached(qc[r], kb[r], vb[r], kp, vp, slots5[i], 128 ** -0.5, dtype=np.float32)
+
+    t = timed(c5, 1)
+    blks = [c["blk"]] * len(c["prefix"])
+    fl = configs.attention_flops(blks, [p + c["blk"] for p in c["prefix"]], 32, 128)
+    by = configs.attention_bytes(blks, [p + c["blk"] for p in c["prefix"]], 32, 32, 128)
+    out["c5_layer"] = dict(seconds=round(t, 3), gflops=round(fl / t / 1e9, 1),
+                           gbs_bf16_equivalent=round(by / t / 1e9, 2))
+    out["cores"] = len(os.sched_getaffinity(0))
+    out["kind"] = "port"
+    return out
+
+
 def profile_run(lens, Hq, Hkv, D, n_layers, dev):
     """Fixed dispatch sequence for hardware-counter runs."""
     from dllm_serve_amd import _capi
@@ -751,6 +819,8 @@ def main() -> None:
         log("CPU baseline (oracle)")
         cpu = cpu_baseline(lens, Hq, Hkv, D)
         cpu["value"] = round(cpu["value"], 4)
+        log("CPU oracle on the other configurations' layer calls")
+        extra["cpu_oracle_other_configs"] = cpu_other_configs()
     # The binding ceiling of the headline kernel: HBM when its arithmetic
     # intensity (algorithmic FLOPs / algorithmic bytes) is below the machine
     # balance peak_flops / peak_bw, else MFMA.

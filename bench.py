@@ -521,7 +521,7 @@ def bench_sampler(dev):
         bufs = [(torch.randn(M, V, generator=g, device=dev) * 1.3).to(torch.bfloat16) for _ in range(nb)]
         x0 = torch.empty(M, dtype=torch.int64, device=dev)
         p = torch.empty(M, dtype=torch.bfloat16, device=dev)
-        ws = torch.empty(_capi.softmax_max_workspace_size(M, V), dtype=torch.uint8, device=dev)
+        ws = None  # the kernel needs no workspace
         state = {"i": 0}
 
         def k8():
@@ -719,18 +719,20 @@ def profile_run(lens, Hq, Hkv, D, n_layers, dev):
     for _ in range(4):
         c5["attend"]()
     del c5
-    # K8 softmax-max over the C2 dense step's 8 x 128 rows of LLaDA logits, two buffers alternating
-    V, M = 126464, 1024
-    g = torch.Generator(device=dev).manual_seed(M)
-    bufs = [(torch.randn(M, V, generator=g, device=dev) * 1.3).to(torch.bfloat16) for _ in range(2)]
-    x0 = torch.empty(M, dtype=torch.int64, device=dev)
-    p = torch.empty(M, dtype=torch.bfloat16, device=dev)
-    ws = torch.empty(_capi.softmax_max_workspace_size(M, V), dtype=torch.uint8, device=dev)
-    for i in range(8):
-        _capi.softmax_max(bufs[i % 2], x0, p, ws)
-    torch.cuda.synchronize()
+    # K8 softmax-max over LLaDA logits, two buffers alternating: the C2 dense step's 8 x 128 rows
+    # (256-thread workgroups), then its block step's 8 x 32 rows (1024-thread workgroups)
+    V = 126464
+    for M in (1024, 256):
+        g = torch.Generator(device=dev).manual_seed(M)
+        bufs = [(torch.randn(M, V, generator=g, device=dev) * 1.3).to(torch.bfloat16) for _ in range(2)]
+        x0 = torch.empty(M, dtype=torch.int64, device=dev)
+        p = torch.empty(M, dtype=torch.bfloat16, device=dev)
+        for i in range(8):
+            _capi.softmax_max(bufs[i % 2], x0, p)
+        torch.cuda.synchronize()
+        del bufs
     log(f"profile run done: 3 x 256 MiB copies, {n_layers} attention launches, {n_layers} RoPE launches "
-        f"({n} tokens), 1 C5 store + 4 C5 block-cached launches, 8 K8 launches ({M} x {V} logits)")
+        f"({n} tokens), 1 C5 store + 4 C5 block-cached launches, 8 + 8 K8 launches (1024 and 256 x {V} logits)")
 
 
 TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "attn_dense_kernel_llada_c2_8x384_counters.md")

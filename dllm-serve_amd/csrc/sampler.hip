@@ -1,6 +1,6 @@
 // K8 / K9: the low-confidence remasking sampler of the diffusion runner.
 //
-// K8 (smx_partial_kernel + smx_final_kernel) reduces each row of bf16 logits
+// K8 (smx_row_kernel) reduces each row of bf16 logits
 // [M, V] to what `x0_p, x0 = torch.max(F.softmax(logits, -1), -1)` returns
 // (dllmserve/engine/model_runner.py:862-863,886-887):
 //   m  = max_j l_j,  s = sum_j exp(l_j - m)                      (f32)
@@ -9,13 +9,14 @@
 // in one read of the logits.  A probability can only round to x0_p when its
 // logit is within 2^-6 of m, and bf16 logits below m are that close to it
 // only when |m| <= 2; so x0 is the first index of the maximal logit unless
-// |m| <= 2, in which case the final kernel rescans the columns before that
-// index for an earlier one whose rounded probability ties.
+// |m| <= 2, in which case the columns before that index are rescanned for an
+// earlier one whose rounded probability ties.
 //
-// Layout: one workgroup reduces `split` consecutive 16-byte chunks of one row
-// (each thread every 256th chunk, four loads in flight) to a record
-// {m, s, first index of m}; the final kernel merges a row's records in one
-// wavefront.  HBM-bound: 2 V bytes per row, read once.
+// Layout: one workgroup per row (1024 threads when there are at most 512
+// rows, else 256); each thread streams every NT-th 16-byte chunk with four
+// loads in flight and keeps a record {m, s, first index of m}; the records
+// are merged across the workgroup and one wavefront finishes the row (the
+// tie rescan included).  HBM-bound: 2 V bytes per row, read once.
 //
 // With a per-row temperature T > 0 the row is first transformed as the
 // reference's add_gumbel_noise does (model_runner.py:592-600):
@@ -40,15 +41,7 @@
 namespace dllm {
 
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kSmxThreads = 256;
 constexpr int kUnmaskMaxWin = 8192;  // SamplingParams caps gen_length at 8192
-
-struct SmxRec {
-  float m;
-  float s;
-  int32_t i;
-  int32_t pad;
-};
 
 __device__ __forceinline__ float fexp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
@@ -130,9 +123,6 @@ struct SmxArgs {
   int M;
   int V;
   int chunks;       // V / 8
-  int split;        // chunks per workgroup
-  int S;            // workgroups per row
-  SmxRec* part;     // [M][S]
   int64_t* x0;
   uint16_t* x0p;
   const double* temp;  // per-row temperature (nullable: no transform)
@@ -140,78 +130,67 @@ struct SmxArgs {
   int64_t row_base;
 };
 
-template <bool GUMBEL>
-__global__ __launch_bounds__(kSmxThreads) void smx_partial_kernel(SmxArgs a) {
-  __shared__ float red_m[kSmxThreads / 64];
-  __shared__ float red_s[kSmxThreads / 64];
-  __shared__ int red_i[kSmxThreads / 64];
-  const int row = blockIdx.x / a.S;
-  const int sp = blockIdx.x - row * a.S;
-  const int c0 = sp * a.split;
-  const int c1 = min(a.chunks, c0 + a.split);
+// Fold columns [8 c0, 8 c1) of one row into the thread's running (m, s, i):
+// thread t takes chunks c0 + t, c0 + t + NT, ..., four 16-byte loads in flight.
+template <bool GUMBEL, int NT>
+__device__ __forceinline__ void smx_scan(const SmxArgs& a, int row, int c0, int c1, float& m, float& s, int& idx) {
   const uint16_t* base = a.logits + (int64_t)row * a.ld;
-  float m = -INFINITY, s = 0.f;
-  int idx = INT_MAX;
   const u32x4_t ninf = {0xff80ff80u, 0xff80ff80u, 0xff80ff80u, 0xff80ff80u};
-  for (int c = c0 + (int)threadIdx.x; c < c1; c += 4 * kSmxThreads) {
+  const double T = GUMBEL ? a.temp[row] : 0.0;
+  const uint64_t rc = GUMBEL ? (uint64_t)(a.row_base + row) * (uint64_t)a.V : 0;
+  for (int c = c0 + (int)threadIdx.x; c < c1; c += 4 * NT) {
     u32x4_t v[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const int cc = c + u * kSmxThreads;
+      const int cc = c + u * NT;
       v[u] = cc < c1 ? ld128_stream(base + 8 * (int64_t)cc) : ninf;
     }
-    if (!GUMBEL) {
 #pragma unroll
-      for (int u = 0; u < 4; ++u) smx_chunk<false>(v[u], 8 * (c + u * kSmxThreads), m, s, idx);
-    } else {
-      const double T = a.temp[row];
-      const uint64_t rc = (uint64_t)(a.row_base + row) * (uint64_t)a.V;
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int e0 = 8 * (c + u * kSmxThreads);
-        if (T > 0.0 && c + u * kSmxThreads < c1)  // padding chunks stay -inf
-          smx_chunk<true>(v[u], e0, m, s, idx, T, a.seed, rc + (uint64_t)e0);
-        else
-          smx_chunk<false>(v[u], e0, m, s, idx);
-      }
+    for (int u = 0; u < 4; ++u) {
+      const int e0 = 8 * (c + u * NT);
+      if (GUMBEL && T > 0.0 && c + u * NT < c1)  // padding chunks stay -inf
+        smx_chunk<true>(v[u], e0, m, s, idx, T, a.seed, rc + (uint64_t)e0);
+      else
+        smx_chunk<false>(v[u], e0, m, s, idx);
     }
   }
+}
+
+// Merge the workgroup's per-thread records; every thread returns the result.
+template <int NT>
+__device__ __forceinline__ void smx_block_reduce(float& m, float& s, int& idx) {
+  __shared__ float red_m[NT / 64];
+  __shared__ float red_s[NT / 64];
+  __shared__ int red_i[NT / 64];
   smx_wave_reduce(m, s, idx);
-  const int wave = threadIdx.x >> 6;
-  if ((threadIdx.x & 63) == 0) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if (lane == 0) {
     red_m[wave] = m;
     red_s[wave] = s;
     red_i[wave] = idx;
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
-    for (int w = 1; w < kSmxThreads / 64; ++w) smx_merge(m, s, idx, red_m[w], red_s[w], red_i[w]);
-    SmxRec r;
-    r.m = m;
-    r.s = s;
-    r.i = idx;
-    r.pad = 0;
-    a.part[(int64_t)row * a.S + sp] = r;
-  }
-}
-
-// One wavefront per row: merge the row's records, then resolve ties of the
-// rounded probabilities when |m| <= 2.
-__global__ __launch_bounds__(256) void smx_final_kernel(SmxArgs a) {
-  const int lane = threadIdx.x & 63;
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= a.M) return;  // uniform per wavefront
-  float m = -INFINITY, s = 0.f;
-  int idx = INT_MAX;
-  for (int k = lane; k < a.S; k += 64) {
-    const SmxRec r = a.part[(int64_t)row * a.S + k];
-    smx_merge(m, s, idx, r.m, r.s, r.i);
+  m = -INFINITY;
+  s = 0.f;
+  idx = INT_MAX;
+  if (lane < NT / 64) {
+    m = red_m[lane];
+    s = red_s[lane];
+    idx = red_i[lane];
   }
   smx_wave_reduce(m, s, idx);
+}
+
+// x0 / x0_p of one row from its merged (m, s, first index of m), by one
+// wavefront: the probability of the maximum is bf16(1/s); when |m| <= 2 an
+// earlier column may round to the same probability, so the columns before
+// the first maximum are rescanned for the earliest such one.
+__device__ void smx_finish(const SmxArgs& a, int row, float m, float s, int idx) {
+  const int lane = threadIdx.x & 63;
   const uint32_t P = f32_to_bf16_bits(1.0f / s);
   int best = idx;
   if (fabsf(m) <= 2.0f && idx != INT_MAX && idx > 0) {
-    // earliest column j < idx with bf16(exp(l_j - m) / s) == P
+    // earliest column j < idx with bf16(exp(v_j - m) / s) == P
     const uint16_t* base = a.logits + (int64_t)row * a.ld;
     const float thr = m - 0.015625f;
     int found = INT_MAX;
@@ -237,6 +216,17 @@ __global__ __launch_bounds__(256) void smx_final_kernel(SmxArgs a) {
     a.x0[row] = best == INT_MAX ? 0 : best;
     a.x0p[row] = (uint16_t)P;
   }
+}
+
+// One workgroup per row: scan, merge and finish in one launch.
+template <bool GUMBEL, int NT>
+__global__ __launch_bounds__(NT) void smx_row_kernel(SmxArgs a) {
+  const int row = blockIdx.x;
+  float m = -INFINITY, s = 0.f;
+  int idx = INT_MAX;
+  smx_scan<GUMBEL, NT>(a, row, 0, a.chunks, m, s, idx);
+  smx_block_reduce<NT>(m, s, idx);
+  if ((threadIdx.x >> 6) == 0) smx_finish(a, row, m, s, idx);
 }
 
 // ---- K9 ---------------------------------------------------------------------
@@ -323,25 +313,15 @@ __global__ __launch_bounds__(256) void lowconf_unmask_kernel(UnmaskArgs a) {
 
 using namespace dllm;
 
-static int smx_splits(int M, int chunks) {
-  // about 8 workgroups per CU in all, each at least 256 chunks (4 KiB)
-  const int want = (2048 + M - 1) / M;
-  const int cap = chunks / kSmxThreads > 1 ? chunks / kSmxThreads : 1;
-  int S = want < cap ? want : cap;
-  if (S > 64) S = 64;
-  if (S < 1) S = 1;
-  return S;
-}
-
 extern "C" size_t dllm_softmax_max_workspace_size(int M, int V) {
-  if (M <= 0 || V <= 0) return 0;
-  const int S = smx_splits(M, (V + 7) / 8);
-  return (size_t)M * S * sizeof(SmxRec);
+  (void)M;
+  (void)V;
+  return 0;  // one workgroup per row: no partial records
 }
 
 static int softmax_max_launch(const char* name, const uint16_t* logits, int64_t ld, int M, int V,
                               const double* row_temperature, uint64_t seed, int64_t row_base, int64_t* x0,
-                              uint16_t* x0_p, void* workspace, size_t workspace_bytes, void* stream) {
+                              uint16_t* x0_p, void* stream) {
   if (M < 0 || V < 0) return fail(DLLM_ERR_INVALID_ARG, "%s: negative size", name);
   if (M == 0) return DLLM_OK;
   if (V == 0 || V % 8 != 0)
@@ -350,50 +330,49 @@ static int softmax_max_launch(const char* name, const uint16_t* logits, int64_t 
   if (!aligned16(logits) || ld % 8 != 0 || ld < V)
     return fail(DLLM_ERR_INVALID_ARG, "%s: logits must be 16-byte aligned with a row stride >= V and a multiple of 8",
                 name);
-  const int chunks = V / 8;
-  const int S = smx_splits(M, chunks);
-  const size_t need = (size_t)M * S * sizeof(SmxRec);
-  if (!workspace || workspace_bytes < need || !aligned16(workspace))
-    return fail(DLLM_ERR_WORKSPACE, "%s: workspace of %zu bytes (16-byte aligned) required, got %zu", name, need,
-                workspace ? workspace_bytes : (size_t)0);
-  if ((int64_t)M * S > INT_MAX) return fail(DLLM_ERR_INVALID_ARG, "%s: too many rows", name);
   SmxArgs a;
   a.logits = logits;
   a.ld = ld;
   a.M = M;
   a.V = V;
-  a.chunks = chunks;
-  a.S = S;
-  a.split = (chunks + S - 1) / S;
-  a.part = reinterpret_cast<SmxRec*>(workspace);
+  a.chunks = V / 8;
   a.x0 = x0;
   a.x0p = x0_p;
   a.temp = row_temperature;
   a.seed = seed;
   a.row_base = row_base;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  if (row_temperature)
-    smx_partial_kernel<true><<<dim3((unsigned)(M * S)), dim3(kSmxThreads), 0, st>>>(a);
-  else
-    smx_partial_kernel<false><<<dim3((unsigned)(M * S)), dim3(kSmxThreads), 0, st>>>(a);
-  int rc = check_launch(name);
-  if (rc != DLLM_OK) return rc;
-  smx_final_kernel<<<dim3((unsigned)((M + 3) / 4)), dim3(256), 0, st>>>(a);
+  const dim3 grid((unsigned)M);
+  // few rows: 1024 threads per row keep enough loads in flight per CU
+  if (M <= 512) {
+    if (row_temperature)
+      smx_row_kernel<true, 1024><<<grid, dim3(1024), 0, st>>>(a);
+    else
+      smx_row_kernel<false, 1024><<<grid, dim3(1024), 0, st>>>(a);
+  } else {
+    if (row_temperature)
+      smx_row_kernel<true, 256><<<grid, dim3(256), 0, st>>>(a);
+    else
+      smx_row_kernel<false, 256><<<grid, dim3(256), 0, st>>>(a);
+  }
   return check_launch(name);
 }
 
 extern "C" int dllm_softmax_max(const uint16_t* logits, int64_t ld, int M, int V, int64_t* x0, uint16_t* x0_p,
                                 void* workspace, size_t workspace_bytes, void* stream) {
-  return softmax_max_launch("dllm_softmax_max", logits, ld, M, V, nullptr, 0, 0, x0, x0_p, workspace,
-                            workspace_bytes, stream);
+  (void)workspace;
+  (void)workspace_bytes;
+  return softmax_max_launch("dllm_softmax_max", logits, ld, M, V, nullptr, 0, 0, x0, x0_p, stream);
 }
 
 extern "C" int dllm_softmax_max_sample(const uint16_t* logits, int64_t ld, int M, int V,
                                        const double* row_temperature, uint64_t seed, int64_t row_base, int64_t* x0,
                                        uint16_t* x0_p, void* workspace, size_t workspace_bytes, void* stream) {
   if (row_base < 0) return fail(DLLM_ERR_INVALID_ARG, "dllm_softmax_max_sample: negative row_base");
+  (void)workspace;
+  (void)workspace_bytes;
   return softmax_max_launch("dllm_softmax_max_sample", logits, ld, M, V, row_temperature, seed, row_base, x0, x0_p,
-                            workspace, workspace_bytes, stream);
+                            stream);
 }
 
 extern "C" int dllm_lowconf_unmask(int64_t* tokens, int64_t n_tokens, const int32_t* seq_params, int n_seq,

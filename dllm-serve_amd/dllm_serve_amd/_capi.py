@@ -209,28 +209,28 @@ def softmax_max_workspace_size(M, V) -> int:
     return int(load().dllm_softmax_max_workspace_size(M, V))
 
 
-def softmax_max(logits, x0, x0_p, workspace):
+def softmax_max(logits, x0, x0_p, workspace=None):
     """K8: x0_p, x0 = max(softmax(logits, -1), -1) of bf16 logits [M, V]
-    (x0 int64 [M], x0_p bf16 [M])."""
+    (x0 int64 [M], x0_p bf16 [M]).  workspace is optional (the kernel needs none)."""
     _require_gpu(logits, x0, x0_p, workspace)
     lib = load()
     M, V = logits.shape
-    ws_bytes = workspace.numel() * workspace.element_size()
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
     rc = lib.dllm_softmax_max(logits.data_ptr(), logits.stride(0), M, V, x0.data_ptr(), x0_p.data_ptr(),
-                              workspace.data_ptr(), ws_bytes, _stream(logits.device))
+                              _ptr(workspace), ws_bytes, _stream(logits.device))
     _check(rc, "dllm_softmax_max")
 
 
-def softmax_max_sample(logits, row_temperature, seed, row_base, x0, x0_p, workspace):
+def softmax_max_sample(logits, row_temperature, seed, row_base, x0, x0_p, workspace=None):
     """K8 with Gumbel noise on the rows whose temperature is > 0
     (row_temperature: float64 [M] on the device, or None)."""
     _require_gpu(logits, row_temperature, x0, x0_p, workspace)
     lib = load()
     M, V = logits.shape
-    ws_bytes = workspace.numel() * workspace.element_size()
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
     rc = lib.dllm_softmax_max_sample(logits.data_ptr(), logits.stride(0), M, V, _ptr(row_temperature),
                                      int(seed) & 0xFFFFFFFFFFFFFFFF, int(row_base), x0.data_ptr(), x0_p.data_ptr(),
-                                     workspace.data_ptr(), ws_bytes, _stream(logits.device))
+                                     _ptr(workspace), ws_bytes, _stream(logits.device))
     _check(rc, "dllm_softmax_max_sample")
 
 

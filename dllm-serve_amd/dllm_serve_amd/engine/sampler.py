@@ -84,8 +84,10 @@ class RemaskSampler:
         self.calls = 0
         self._ws = None
 
-    def _workspace(self, M: int, V: int, device) -> torch.Tensor:
+    def _workspace(self, M: int, V: int, device) -> Optional[torch.Tensor]:
         need = _capi.softmax_max_workspace_size(M, V)
+        if need == 0:
+            return None
         if self._ws is None or self._ws.numel() < need or self._ws.device != device:
             self._ws = torch.empty(max(need, 16), dtype=torch.uint8, device=device)
         return self._ws

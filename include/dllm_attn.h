@@ -198,8 +198,9 @@ int dllm_rope_neox(const dllm_bf16* q_in, int64_t q_in_stride, dllm_bf16* q_out,
  *   x0_p[r] = max_j P_j = bf16(1 / s),  x0[r] = min { j : P_j == x0_p[r] }
  * (torch.max returns the first maximal index).  Rows holding NaN or only
  * -inf give unspecified results (torch's are NaN).  V must be a multiple of
- * 8; logits 16-byte aligned, ld a multiple of 8 and >= V.  workspace must
- * hold dllm_softmax_max_workspace_size(M, V) bytes, 16-byte aligned.
+ * 8; logits 16-byte aligned, ld a multiple of 8 and >= V.  One workgroup
+ * reduces each row, so dllm_softmax_max_workspace_size returns 0 and
+ * workspace may be null (the arguments keep the signature stable).
  */
 size_t dllm_softmax_max_workspace_size(int M, int V);
 int dllm_softmax_max(const dllm_bf16* logits, int64_t ld, int M, int V, int64_t* x0, dllm_bf16* x0_p,

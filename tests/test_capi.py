@@ -113,16 +113,16 @@ def test_sampler_validation_without_gpu():
     lib = _capi.load()
     P = ctypes.c_void_p
     fake = P(4096)
-    assert _capi.softmax_max_workspace_size(1024, 126464) == 1024 * 2 * 16
-    assert _capi.softmax_max_workspace_size(64, 126464) == 64 * 32 * 16
-    assert _capi.softmax_max_workspace_size(0, 126464) == 0
-    ws = _capi.softmax_max_workspace_size(64, 126464)
+    # one workgroup per row: no workspace at any size, and a null one is accepted
+    assert _capi.softmax_max_workspace_size(1024, 126464) == 0
+    assert _capi.softmax_max_workspace_size(64, 126464) == 0
+    ws = 0
     rc, msg = _err(lib.dllm_softmax_max(fake, 126464, 64, 126460, fake, fake, fake, ws, None))
     assert rc == _capi.DLLM_ERR_UNSUPPORTED and "multiple of 8" in msg
     rc, msg = _err(lib.dllm_softmax_max(fake, 126456, 64, 126464, fake, fake, fake, ws, None))
     assert rc == _capi.DLLM_ERR_INVALID_ARG and "stride" in msg
-    rc, msg = _err(lib.dllm_softmax_max(fake, 126464, 64, 126464, fake, fake, fake, ws - 16, None))
-    assert rc == _capi.DLLM_ERR_WORKSPACE and "workspace" in msg
+    rc, msg = _err(lib.dllm_softmax_max(None, 126464, 64, 126464, fake, fake, None, 0, None))
+    assert rc == _capi.DLLM_ERR_INVALID_ARG and "null" in msg
     assert lib.dllm_softmax_max(fake, 126464, 0, 126464, fake, fake, None, 0, None) == 0
     rc, msg = _err(lib.dllm_lowconf_unmask(fake, 100, fake, 4, 8193, fake, fake, 100, 126336, None, None))
     assert rc == _capi.DLLM_ERR_UNSUPPORTED and "8192" in msg

@@ -334,6 +334,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(OCC, OC
   constexpr int DMA_TILE = 2 * DMA_PER_WAVE;               // this wave's DMA instructions per tile, K and V
   static_assert(TK % 32 == 0, "tile shape");
   static_assert(NDMA % NW == 0 || (NW > NDMA && ST == 2), "an uneven DMA split needs the full wait of two stages");
+  constexpr bool QDMA = NQ == 1 && NW == 4 * OCC;  // one workgroup per CU
+  constexpr int QOFF = ST * STAGE;                 // Q rows after the K/V stages (NW * 8 KiB)
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int L = xcd_remap(blockIdx.x, gridDim.x);
   if (L >= a.logical_blocks) return;
@@ -385,6 +387,10 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(OCC, OC
     if (j < ntiles) issue(lds + j * STAGE, j * TK);
 
   // Q^T fragments; rows past the segment read as zero through the buffer bound.
+  // A workgroup that owns its CU (NW == 4 * OCC) has LDS to spare: its Q rows
+  // are DMA'd in whole 256-byte rows (4 rows per instruction, the K tile's
+  // swizzle) and the fragments read back like K operands.  Otherwise every
+  // load instruction carries 32-byte pieces of 32 rows straight to VGPRs.
   bf16x8_t qf[NQ][8];
   int tokq[NQ], headq[NQ];
   bool okq[NQ];
@@ -392,6 +398,33 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(OCC, OC
     const uint32_t qS = (uint32_t)(a.q_stride * 2);
     const uint32_t qbytes = Lq > 0 ? (uint32_t)Lq * qS : 0u;
     const __amdgpu_buffer_rsrc_t qrs = make_rsrc(a.q + (int64_t)qrow0 * a.q_stride, qbytes);
+    if constexpr (QDMA) {
+      // instruction j, lane L: row R = 4j + L/16 of this wave's 32, physical
+      // chunk L%16 = logical chunk (L%16) ^ (R & 15)
+      const int rl = lane >> 4, P = lane & 15;
+      const int m0 = m_base + wave * 32 + rl;
+      int tok = m0 / g, rem = m0 - tok * g;
+      const int q4 = 4 / g, r4 = 4 - q4 * g;  // m advances by 4 per instruction
+      uint8_t* qdst = lds + QOFF + wave * 8192;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int R = 4 * j + rl;
+        const uint32_t off = m0 + 4 * j < M
+                                 ? (uint32_t)tok * qS + (uint32_t)((hkv * g + rem) * HD * 2) +
+                                       (uint32_t)((P ^ (R & 15)) * 16)
+                                 : qbytes;
+        dma16(qrs, qdst + j * 1024, off);
+        tok += q4;
+        rem += r4;
+        if (rem >= g) {
+          rem -= g;
+          ++tok;
+        }
+      }
+      okq[0] = m_base + wave * 32 + lrow < M;
+      tokq[0] = 0;
+      headq[0] = 0;
+    } else {
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
       const int m = m_base + (wave * NQ + q) * 32 + lrow;
@@ -402,6 +435,15 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(OCC, OC
 #pragma unroll
       for (int kk = 0; kk < 8; ++kk) qf[q][kk] = as_bf16x8(bload(qrs, qoff + (uint32_t)kk * 32u, 0u));
     }
+    }
+  }
+  if constexpr (QDMA) {
+    vm_wait<0>();  // this wave's Q rows and its share of tile 0
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk)
+      qf[0][kk] = as_bf16x8(
+          *reinterpret_cast<const u32x4_t*>(lds + QOFF + wave * 8192 + (ad.kbase ^ (uint32_t)(32 * kk))));
   }
 
   DenseState<NQ> st;
@@ -444,7 +486,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(OCC, OC
     // The wave's 32 rows x 256 bytes land in its own 8 KiB of the (now free)
     // K/V stages, chunks XOR-swizzled by row; read back, instruction j
     // carries rows 4j .. 4j+3, one 16-byte chunk per lane.
-    // O staging needs NW * 8 KiB: the launch gives max(ST * STAGE, NW * 8192) bytes of LDS
+    // O staging needs NW * 8 KiB at the front of LDS; the launch gives at least that
     const float l_tot = pair_sum32(st.l_run[0]);
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
     __syncthreads();  // every wavefront is done reading the K/V stages
@@ -919,7 +961,10 @@ extern "C" int dllm_attn_varlen_fwd(const dllm_bf16* q, const dllm_bf16* k, cons
   auto kern = wide ? attn_dense_kernel<8, 1, DENSE_ST, 64, 2>
                    : (one_wg ? attn_dense_kernel<12, 1, DENSE_ST, 32, 3> : attn_dense_kernel<4, 1, DENSE_ST, 32, 3>);
   int lds_bytes = DENSE_ST * 2 * (wide ? 64 : 32) * 256;
-  if (nw * 8192 > lds_bytes) lds_bytes = nw * 8192;  // O staging
+  if (wide || one_wg)
+    lds_bytes += nw * 8192;  // Q rows after the stages (one workgroup per CU); O staging reuses the front
+  else if (nw * 8192 > lds_bytes)
+    lds_bytes = nw * 8192;  // O staging
   if ((rc = set_lds(kern, lds_bytes, name))) return rc;
   const int nb = (int)((logical + 7) / 8 * 8);
   kern<<<dim3(nb), dim3(64 * nw), lds_bytes, reinterpret_cast<hipStream_t>(stream)>>>(a);

@@ -749,12 +749,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   __syncthreads();
 
   // ---- merge the four wavefronts' states (each holds 32 M rows x its keys)
+  // ored rows (one per (wavefront, d)) are kMergeLd floats apart: the read
+  // below has lanes 0..31 on rows q = 0..31 of one d and lanes 32..63 on
+  // d + 16, i.e. 16 * kMergeLd floats further, which puts the two halves on
+  // disjoint banks (a 32-float pitch would put all of them on the same ones).
+  constexpr int kMergeLd = 34;
+  static_assert((8 * 32 + 4 * HD * kMergeLd) * 4 <= 2 * CK_STAGE, "the merge area fits in the two stages");
   const float m_run = st.m_run[0];
   const float l_tot = pair_sum32(st.l_run[0]);
   float* red = reinterpret_cast<float*>(lds);
   float* red_m = red;             // [4][32]
   float* red_l = red + 4 * 32;    // [4][32]
-  float* ored = red + 8 * 32;     // [4][128][32]
+  float* ored = red + 8 * 32;     // [4][128][kMergeLd]
   if (hl == 0) {
     red_m[wave * 32 + lrow] = m_run;
     red_l[wave * 32 + lrow] = l_tot;
@@ -770,11 +776,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int d = db * 32 + 8 * (i >> 2) + 4 * hl + (i & 3);
-      ored[(wave * HD + d) * 32 + lrow] = st.oacc[0][db][i] * fac;
+      ored[(wave * HD + d) * kMergeLd + lrow] = st.oacc[0][db][i] * fac;
     }
   __syncthreads();
-  const int q = tid >> 3;
-  const int d0 = (tid & 7) * 16;
+  const int q = tid & 31;
+  const int d0 = (tid >> 5) * 16;
   float mq = -INFINITY;
 #pragma unroll
   for (int w = 0; w < 4; ++w) mq = fmaxf(mq, red_m[w * 32 + q]);
@@ -790,7 +796,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   for (int i = 0; i < 16; ++i) {
     float sum = 0.f;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) sum += ored[(w * HD + d0 + i) * 32 + q];
+    for (int w = 0; w < 4; ++w) sum += ored[(w * HD + d0 + i) * kMergeLd + q];
     acc[i] = sum;
   }
   const int mrow = m_base + q;
@@ -816,7 +822,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         f32x4_t v4 = {acc[i], acc[i + 1], acc[i + 2], acc[i + 3]};
         *reinterpret_cast<f32x4_t*>(po + i) = v4;
       }
-      if ((tid & 7) == 0) {
+      if (d0 == 0) {  // one writer per row
         const int64_t nrec = (int64_t)a.n_seg * a.Hkv * a.mtiles * a.n_split;
         float* pml = a.ws + nrec * 32 * HD + (Prec * 32 + q) * 2;
         pml[0] = mq;

@@ -69,6 +69,26 @@ def test_varlen_long_key_streams(dev, lens, Hq, Hkv):
     assert_attn_close(o, ref, f"lens={lens}")
 
 
+@pytest.mark.parametrize("lens,Hq,Hkv", [
+    ([150, 129, 191, 5], 4, 2),     # g = 2; the longest segment gives 382 M rows: 12-wavefront launch
+    ([100, 128, 86, 1], 6, 2),      # g = 3, 384 M rows
+    ([52, 76, 60], 10, 2),          # g = 5, 380 M rows
+    ([43, 64, 50], 12, 2),          # g = 6, 384 M rows
+    ([33, 48, 40], 16, 2),          # g = 8, 384 M rows
+    ([2100, 37], 3, 1),             # g = 3, keys >= 2048: 8-wavefront launch
+    ([2050, 300], 5, 1),            # g = 5, the same
+])
+def test_varlen_gqa_ratios_on_the_cu_owning_launches(dev, lens, Hq, Hkv):
+    """The 12- and 8-wavefront launches stage Q through LDS: M row m is token
+    m / g, head hkv * g + m % g for every group size, rows past a segment read
+    zero."""
+    print(f"varlen gqa lens={lens} Hq={Hq} Hkv={Hkv}", flush=True)
+    q, k, v, cu = configs.packed_qkv(lens, Hq, Hkv, 128, seed=7 * sum(lens) + Hq)
+    o = _run_varlen(q, k, v, cu, dev)
+    ref = oatt.varlen(to_np(q), to_np(k), to_np(v), cu.numpy(), cu.numpy(), 128 ** -0.5, dtype=np.float32)
+    assert_attn_close(o, ref, f"lens={lens} Hq={Hq} Hkv={Hkv}")
+
+
 @pytest.mark.parametrize("lq,lk", [([40, 7, 300], [100, 2200, 5]), ([128, 64], [64, 128])])
 def test_varlen_different_q_and_k_lengths(dev, lq, lk):
     """cu_seqlens_q != cu_seqlens_k, as flash_attn_varlen_func allows."""

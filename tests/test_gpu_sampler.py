@@ -50,6 +50,7 @@ def _check_k8(logits_host_bits, x0, p):
     (1024, 126464, 1.3, 0),     # C2 dense step row count
     (96, 152064, 2.0, 0),       # Dream vocabulary
     (300, 4096, 0.3, 0),        # |max| <= 2: the rounding-tie rescan runs on every row
+    (513, 4104, 0.4, 8),        # more than 512 rows: 256-thread workgroups, rescan rows, strided
     (37, 264, 0.5, 8),
     (5, 8, 1.0, 0),
 ])

@@ -662,9 +662,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     return m;
   };
 
-  // ---- Q^T fragments, loaded before the first slot fetch: the wait for
-  // those slots (in-order completion) retires them, so no wait on q remains
-  // inside the tile loop.
+  // ---- prologue: the slots of the first three tiles and the Q^T fragments
+  // in one batch, one full wait (which also retires q for the compiler's own
+  // wait tracking, so no wait on q remains inside the tile loop), then D(0)
+  // and D(1) together: tile 1 does not wait a second round trip.  Slot
+  // fetches past the key range read a clamped, valid index and go unused.
+  int s0[8], s1[8];
+  int slot_ahead[8];          // slots of the next tile to issue: S(2) here
+  fetch_slots(s0, kbeg);
+  fetch_slots(s1, kbeg + CK_TILE);
+  fetch_slots(slot_ahead, kbeg + 2 * CK_TILE);
   const int m = m_base + lrow;
   const bool m_ok = m < M;
   const int tok = m_ok ? m / g : 0;
@@ -679,28 +686,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     for (int kk = 0; kk < 8; ++kk) qf[0][kk] = as_bf16x8(bload(qrs, qoff + (uint32_t)kk * 32u, 0u));
   }
   const int ntiles = (kend - kbeg + CK_TILE - 1) / CK_TILE;
-  int slot_ahead[8];          // slots of the next tile to issue
   uint32_t bad_t0 = 0, bad_t1 = 0;  // invalid-row masks of tiles t and t+1
-  {
-    int cur[8];
-    fetch_slots(cur, kbeg);
-    vm_wait<0>();  // q and S(0); the compiler sees q retired on every path
-    slots_ready(cur);
-    if (ntiles > 0) {
-      bad_t0 = invalid_rows(kbeg, cur);
-      issue(lds, kbeg, cur);                                   // D(0)
-    }
-    if (ntiles > 1) {
-      fetch_slots(cur, kbeg + CK_TILE);
-      if (ntiles > 2) fetch_slots(slot_ahead, kbeg + 2 * CK_TILE);   // S(2) before D(1)
-      if (ntiles > 2)
-        vm_wait<8>();  // S(1) (and D(0)); S(2) may stay in flight
-      else
-        vm_wait<0>();
-      slots_ready(cur);
-      bad_t1 = invalid_rows(kbeg + CK_TILE, cur);
-      issue(lds + CK_STAGE, kbeg + CK_TILE, cur);              // D(1)
-    }
+  vm_wait<0>();  // S(0..2) and q
+  slots_ready(s0);
+  slots_ready(s1);
+  slots_ready(slot_ahead);
+  if (ntiles > 0) {
+    bad_t0 = invalid_rows(kbeg, s0);
+    issue(lds, kbeg, s0);                                    // D(0)
+  }
+  if (ntiles > 1) {
+    bad_t1 = invalid_rows(kbeg + CK_TILE, s1);
+    issue(lds + CK_STAGE, kbeg + CK_TILE, s1);               // D(1)
   }
 
   DenseAddr ad;
@@ -717,13 +714,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   for (int t = 0; t < ntiles; ++t) {
     const int k0 = kbeg + t * CK_TILE;
     // D(t) has landed once at most the operations issued after it -- S(t+2)
-    // and D(t+1), when they exist -- are outstanding.
-    if (t + 2 < ntiles)
-      vm_wait<24>();
-    else if (t + 1 < ntiles)
+    // and D(t+1), when they exist -- are outstanding.  At t = 0 only D(1)
+    // follows D(0) (the prologue retired S(2) before issuing both).
+    if (t + 1 >= ntiles)
+      vm_wait<0>();
+    else if (t == 0 || t + 2 >= ntiles)
       vm_wait<16>();
     else
-      vm_wait<0>();
+      vm_wait<24>();
     uint8_t* cur = lds + (t & 1) * CK_STAGE + wave * 32 * 256;  // this wave's 32 rows
     const int k_valid = kend - (k0 + 32 * wave);
     if (k_valid < 32 || bad_t0 != 0)

@@ -5,7 +5,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import assert_attn_close, bits, to_np
+from helpers import assert_attn_close, to_np
 
 from oracle import attention as oatt
 from oracle import configs

@@ -2,7 +2,6 @@
 maps, the per-step launch plan and the no-CPU-fallback rule.  Expected
 values are hand-derived from the reference's rules (sparse/state.py:44-104,
 engine/sequence.py:87-152, engine/model_runner.py:257-302)."""
-import numpy as np
 import pytest
 import torch
 

@@ -876,6 +876,7 @@ static const float kLog2e = 1.4426950408889634f;
 // is long enough (max_seqlen_k >= 2048) to amortise the larger tiles.
 constexpr int DENSE_ST = 2;
 constexpr int DENSE_LONG_K = 2048;
+constexpr int kOneWgMinPairs = 160;  // (segment, KV head) pairs for the 12-wavefront launch
 
 static int common_checks(const char* name, const void* q, const void* k, const void* v, const void* o, int Hq,
                          int Hkv, int D, int64_t qs, int64_t ks, int64_t vs, int64_t os) {
@@ -944,9 +945,12 @@ extern "C" int dllm_attn_varlen_fwd(const dllm_bf16* q, const dllm_bf16* k, cons
   const bool wide = max_seqlen_k >= DENSE_LONG_K;
   // (segment, KV head) pairs of 257..384 M rows: one 12-wavefront workgroup
   // each, so the pair's K/V tiles are read into LDS once instead of by three
-  // workgroups (3 % faster for 8 x 384 tokens, 32 heads).
+  // workgroups (3 % faster for 8 x 384 tokens, 32 heads) -- when there are
+  // enough pairs to occupy most of the 256 CUs.  Fewer pairs run faster as
+  // three 4-wavefront workgroups each (32 heads x 384 tokens: 1 sequence
+  // 12.6 vs 19.8 us, 4 sequences 20.2 vs 23.3 us; 6 sequences 27.4 vs 25.1).
   const int64_t m_rows = (int64_t)max_seqlen_q * (Hq / Hkv);
-  const bool one_wg = !wide && m_rows > 256 && m_rows <= 384;
+  const bool one_wg = !wide && m_rows > 256 && m_rows <= 384 && (int64_t)n_seg * Hkv >= kOneWgMinPairs;
   const int nw = wide ? 8 : (one_wg ? 12 : 4);
   const int bm = 32 * nw;
   a.mtiles = (int)(((int64_t)max_seqlen_q * a.g + bm - 1) / bm);

@@ -46,8 +46,9 @@ def test_c1_single_layer(dev):
     ([200, 517, 1], 28, 4),                            # Dream GQA, g = 7
     ([96, 160], 8, 2),                                 # g = 4
     ([1000], 4, 4),
-    ([300, 384, 1, 257, 383], 16, 16),               # 257..384 M rows: one 12-wavefront workgroup per pair
-    ([64, 96, 7], 16, 4),                              # the same launch with GQA (96 x 4 = 384 M rows)
+    ([300, 384, 1, 257, 383], 32, 32),               # 257..384 M rows, 160 pairs: one 12-wavefront workgroup each
+    ([64, 96, 7, 90] * 10, 16, 4),                     # the same launch with GQA (96 x 4 = 384 M rows, 160 pairs)
+    ([300, 384, 1, 257, 383], 16, 16),               # the same rows, 80 pairs: three 4-wavefront workgroups each
 ])
 def test_varlen_ragged(dev, lens, Hq, Hkv):
     print(f"varlen lens={lens} Hq={Hq} Hkv={Hkv}", flush=True)
@@ -70,13 +71,13 @@ def test_varlen_long_key_streams(dev, lens, Hq, Hkv):
 
 
 @pytest.mark.parametrize("lens,Hq,Hkv", [
-    ([150, 129, 191, 5], 4, 2),     # g = 2; the longest segment gives 382 M rows: 12-wavefront launch
-    ([100, 128, 86, 1], 6, 2),      # g = 3, 384 M rows
-    ([52, 76, 60], 10, 2),          # g = 5, 380 M rows
-    ([43, 64, 50], 12, 2),          # g = 6, 384 M rows
-    ([33, 48, 40], 16, 2),          # g = 8, 384 M rows
-    ([2100, 37], 3, 1),             # g = 3, keys >= 2048: 8-wavefront launch
-    ([2050, 300], 5, 1),            # g = 5, the same
+    ([150, 129, 191, 5] * 5, 16, 8),   # g = 2; 382 M rows, 160 (segment, KV head) pairs: 12-wavefront launch
+    ([100, 128, 86, 1] * 5, 24, 8),    # g = 3, 384 M rows
+    ([52, 76, 60, 3] * 5, 40, 8),      # g = 5, 380 M rows
+    ([43, 64, 50, 2] * 5, 48, 8),      # g = 6, 384 M rows
+    ([33, 48, 40, 1] * 5, 64, 8),      # g = 8, 384 M rows
+    ([2100, 37], 3, 1),                # g = 3, keys >= 2048: 8-wavefront launch
+    ([2050, 300], 5, 1),               # g = 5, the same
 ])
 def test_varlen_gqa_ratios_on_the_cu_owning_launches(dev, lens, Hq, Hkv):
     """The 12- and 8-wavefront launches stage Q through LDS: M row m is token

@@ -32,6 +32,16 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) {
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
   return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)f);
 }
+// f64 -> f32 (round to nearest even) -> bf16 (round to nearest even): two
+// roundings, as torch's double -> bfloat16 conversion does.  The empty asm
+// keeps the compiler from merging the two conversions into a single
+// double -> bf16 rounding (which it lowers through round-to-odd); the two
+// differ when the f32 value lands exactly on a bf16 midpoint.
+__device__ __forceinline__ uint32_t f64_to_bf16_bits_2step(double x) {
+  float f = (float)x;
+  asm volatile("" : "+v"(f));
+  return f32_to_bf16_bits(f);
+}
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
 }

@@ -80,7 +80,7 @@ __device__ __forceinline__ float gumbel_value(float l, double T, uint64_t seed, 
   const double nl = -log(u);
   const double g = T == 1.0 ? nl : pow(nl, T);
   const double v = exp((double)l) / g;
-  return bf16_bits_to_f32(f32_to_bf16_bits((float)v));
+  return bf16_bits_to_f32(f64_to_bf16_bits_2step(v));
 }
 
 // Fold 8 logits (one 16-byte chunk starting at column e0) into the running

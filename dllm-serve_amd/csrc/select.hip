@@ -50,7 +50,7 @@ __device__ __forceinline__ Job load_job(const int32_t* jobs, int j) {
 __device__ __forceinline__ int cand_row(const Job& jb, int j) { return j < jb.bs ? j : j + jb.bl; }
 
 // f64 -> f32 (round to nearest even) -> bf16 (round to nearest even)
-__device__ __forceinline__ uint32_t f64_to_bf16_bits(double x) { return f32_to_bf16_bits((float)x); }
+__device__ __forceinline__ uint32_t f64_to_bf16_bits(double x) { return f64_to_bf16_bits_2step(x); }
 
 // grid (n_job, Hq), block 128: qbar[h][d] = bf16(f32(sum_t q[bs+t][h][d] / bl))
 __global__ __launch_bounds__(128) void qbar_kernel(SelArgs a) {

@@ -160,7 +160,13 @@ def _select_cases(n=8, seed=55):
     return out
 
 
-@pytest.mark.parametrize("case", _select_cases(), ids=lambda c: f"s{c[0]}")
+# A raw score whose f64 sum (8.65625000006) rounds to f32 exactly onto a bf16
+# midpoint: the two-step rule gives 8.625, a single f64 -> bf16 rounding 8.6875
+# (candidate 340 of KV head 3 then moved ahead of two higher-ranked ones).
+SELECT_REGRESSIONS = [(3, 4, 643, 16, 4, 0.75, True, 1)]
+
+
+@pytest.mark.parametrize("case", _select_cases() + SELECT_REGRESSIONS, ids=lambda c: f"s{c[0]}-{c[2]}")
 def test_fuzz_select_store(dev, case):
     i, Lb, Kc, Hq, Hkv, ratio, hs, pk = case
     n_keep = min(max(1, int(Kc * ratio)), Kc)

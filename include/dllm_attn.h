@@ -88,7 +88,7 @@ int dllm_load_kvcache(dllm_bf16* key, int64_t key_stride_tok,
  * sizes the grid).  A segment may span at most 4 GiB of q, k or v.  D must be 128;
  * Hq must be a multiple of Hkv.  Pointers must be 16-byte aligned and the
  * token strides multiples of 8 elements.  Rows of o outside the segments are
- * not written.
+ * not written; the rows of a segment with no keys are written as zeros.
  */
 int dllm_attn_varlen_fwd(const dllm_bf16* q, const dllm_bf16* k, const dllm_bf16* v, dllm_bf16* o,
                          const int32_t* cu_q, const int32_t* cu_k, const int32_t* seg_ids,

@@ -18,9 +18,12 @@ from . import select as _sel
 
 
 def segment(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float, dtype=np.float64) -> np.ndarray:
-    """q [Lq,Hq,D], k/v [Lk,Hkv,D] -> o [Lq,Hq,D] (math in `dtype`)."""
+    """q [Lq,Hq,D], k/v [Lk,Hkv,D] -> o [Lq,Hq,D] (math in `dtype`).  With no
+    keys the softmax is empty; the rows are zero (the C ABI's convention)."""
     Lq, Hq, D = q.shape
     Lk, Hkv, _ = k.shape
+    if Lk == 0:
+        return np.zeros((Lq, Hq, D), dtype=dtype)
     g = Hq // Hkv
     qd = q.astype(dtype)
     kd = np.repeat(k.astype(dtype), g, axis=1)  # head h reads KV head h // g

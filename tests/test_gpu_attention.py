@@ -90,7 +90,8 @@ def test_varlen_gqa_ratios_on_the_cu_owning_launches(dev, lens, Hq, Hkv):
     assert_attn_close(o, ref, f"lens={lens} Hq={Hq} Hkv={Hkv}")
 
 
-@pytest.mark.parametrize("lq,lk", [([40, 7, 300], [100, 2200, 5]), ([128, 64], [64, 128])])
+@pytest.mark.parametrize("lq,lk", [([40, 7, 300], [100, 2200, 5]), ([128, 64], [64, 128]),
+                                   ([5, 40, 9], [0, 70, 0])])   # segments without keys give zero rows
 def test_varlen_different_q_and_k_lengths(dev, lq, lk):
     """cu_seqlens_q != cu_seqlens_k, as flash_attn_varlen_func allows."""
     print(f"varlen lq={lq} lk={lk}", flush=True)

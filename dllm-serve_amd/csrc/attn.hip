@@ -554,6 +554,103 @@ __device__ __forceinline__ void gdma16(const void* g, uint8_t* lds_dst) {
   __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds_dst, 16, 0, kStreamAux);
 }
 
+// The four wavefronts' softmax states of one workgroup (each holds the same
+// 32 M rows over its own keys) merged in LDS, normalised and written to o --
+// or, when the keys are split across workgroups, written as a partial record
+// for attn_combine_kernel.  Every thread of the workgroup calls it once.
+__device__ __forceinline__ void cached_merge_store(const AttnArgs& a, uint8_t* lds, const DenseState<1>& st, int s,
+                                                   int hkv, int mt, int split, int qrow0, int M, int m_base, int g) {
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int lrow = lane & 31;
+  const int hl = lane >> 5;
+  __syncthreads();
+
+  // ---- merge the four wavefronts' states (each holds 32 M rows x its keys)
+  // ored rows (one per (wavefront, d)) are kMergeLd floats apart: the read
+  // below has lanes 0..31 on rows q = 0..31 of one d and lanes 32..63 on
+  // d + 16, i.e. 16 * kMergeLd floats further, which puts the two halves on
+  // disjoint banks (a 32-float pitch would put all of them on the same ones).
+  constexpr int kMergeLd = 34;
+  static_assert((8 * 32 + 4 * HD * kMergeLd) * 4 <= 2 * CK_STAGE, "the merge area fits in the two stages");
+  const float m_run = st.m_run[0];
+  const float l_tot = pair_sum32(st.l_run[0]);
+  float* red = reinterpret_cast<float*>(lds);
+  float* red_m = red;             // [4][32]
+  float* red_l = red + 4 * 32;    // [4][32]
+  float* ored = red + 8 * 32;     // [4][128][kMergeLd]
+  if (hl == 0) {
+    red_m[wave * 32 + lrow] = m_run;
+    red_l[wave * 32 + lrow] = l_tot;
+  }
+  __syncthreads();
+  float m_all = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) m_all = fmaxf(m_all, red_m[w * 32 + lrow]);
+  const float m_all_use = (m_all == -INFINITY) ? 0.f : m_all;
+  const float fac = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run - m_all_use);
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int d = db * 32 + 8 * (i >> 2) + 4 * hl + (i & 3);
+      ored[(wave * HD + d) * kMergeLd + lrow] = st.oacc[0][db][i] * fac;
+    }
+  __syncthreads();
+  const int q = tid & 31;
+  const int d0 = (tid >> 5) * 16;
+  float mq = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) mq = fmaxf(mq, red_m[w * 32 + q]);
+  const float mq_use = (mq == -INFINITY) ? 0.f : mq;
+  float lq = 0.f;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const float mw = red_m[w * 32 + q];
+    lq += (mw == -INFINITY) ? 0.f : red_l[w * 32 + q] * __builtin_amdgcn_exp2f(mw - mq_use);
+  }
+  float acc[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    float sum = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) sum += ored[(w * HD + d0 + i) * kMergeLd + q];
+    acc[i] = sum;
+  }
+  const int mrow = m_base + q;
+  if (mrow < M) {
+    const int tq = mrow / g;
+    const int hq = hkv * g + (mrow - tq * g);
+    if (a.n_split == 1) {
+      const float inv = lq > 0.f ? 1.f / lq : 0.f;
+      uint16_t* op = a.o + (int64_t)(qrow0 + tq) * a.o_stride + hq * HD + d0;
+      u32x4_t w0, w1;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        w0[w] = cvt_pk_bf16(acc[2 * w] * inv, acc[2 * w + 1] * inv);
+        w1[w] = cvt_pk_bf16(acc[8 + 2 * w] * inv, acc[8 + 2 * w + 1] * inv);
+      }
+      st128(op, w0);
+      st128(op + 8, w1);
+    } else {
+      const int64_t Prec = (((int64_t)s * a.Hkv + hkv) * a.mtiles + mt) * a.n_split + split;
+      float* po = a.ws + (Prec * 32 + q) * HD + d0;
+#pragma unroll
+      for (int i = 0; i < 16; i += 4) {
+        f32x4_t v4 = {acc[i], acc[i + 1], acc[i + 2], acc[i + 3]};
+        *reinterpret_cast<f32x4_t*>(po + i) = v4;
+      }
+      if (d0 == 0) {  // one writer per row
+        const int64_t nrec = (int64_t)a.n_seg * a.Hkv * a.mtiles * a.n_split;
+        float* pml = a.ws + nrec * 32 * HD + (Prec * 32 + q) * 2;
+        pml[0] = mq;
+        pml[1] = lq;
+      }
+    }
+  }
+}
+
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void attn_cached_kernel(AttnArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int L = xcd_remap(blockIdx.x, gridDim.x);
@@ -590,7 +687,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   const uint32_t kchunk = (uint32_t)((P ^ rl) * 16);
   const uint32_t vchunk = (uint32_t)((P ^ (4 * rl)) * 16);
   const int64_t row_elems = (int64_t)a.Hkv * HD;
-  const int32_t* sp = n_c > 0 ? a.slots + slot_base : a.slot_off;  // a valid dummy when there are none
+  // without a cache (cache_slots = 0, slots may be null) every cached row is
+  // outside it: the fetches then read slot_off[0], a valid dummy
+  const bool have_slots = n_c > 0 && a.slots != nullptr && a.cache_slots > 0;
+  const int32_t* sp = have_slots ? a.slots + slot_base : a.slot_off;
   // Per-wave pipeline (a wavefront DMAs and reads only its own 32 rows of a
   // tile, so no workgroup barrier is needed until the merge): the slots of
   // tile t+2 are fetched before tile t+1's DMA is issued, so that after
@@ -608,7 +708,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int kidx = k0 + 32 * wave + 4 * j + rl;
-      const int32_t* src = sp + min(max(kidx, 0), max(n_c - 1, 0));
+      const int32_t* src = have_slots ? sp + min(max(kidx, 0), n_c - 1) : sp;
       asm volatile("global_load_dword %0, %1, off" : "=v"(dst[j]) : "v"(src) : "memory");
     }
   };
@@ -744,90 +844,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     bad_t0 = bad_t1;
     bad_t1 = bad_t2;
   }
-  __syncthreads();
-
-  // ---- merge the four wavefronts' states (each holds 32 M rows x its keys)
-  // ored rows (one per (wavefront, d)) are kMergeLd floats apart: the read
-  // below has lanes 0..31 on rows q = 0..31 of one d and lanes 32..63 on
-  // d + 16, i.e. 16 * kMergeLd floats further, which puts the two halves on
-  // disjoint banks (a 32-float pitch would put all of them on the same ones).
-  constexpr int kMergeLd = 34;
-  static_assert((8 * 32 + 4 * HD * kMergeLd) * 4 <= 2 * CK_STAGE, "the merge area fits in the two stages");
-  const float m_run = st.m_run[0];
-  const float l_tot = pair_sum32(st.l_run[0]);
-  float* red = reinterpret_cast<float*>(lds);
-  float* red_m = red;             // [4][32]
-  float* red_l = red + 4 * 32;    // [4][32]
-  float* ored = red + 8 * 32;     // [4][128][kMergeLd]
-  if (hl == 0) {
-    red_m[wave * 32 + lrow] = m_run;
-    red_l[wave * 32 + lrow] = l_tot;
-  }
-  __syncthreads();
-  float m_all = -INFINITY;
-#pragma unroll
-  for (int w = 0; w < 4; ++w) m_all = fmaxf(m_all, red_m[w * 32 + lrow]);
-  const float m_all_use = (m_all == -INFINITY) ? 0.f : m_all;
-  const float fac = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run - m_all_use);
-#pragma unroll
-  for (int db = 0; db < 4; ++db)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int d = db * 32 + 8 * (i >> 2) + 4 * hl + (i & 3);
-      ored[(wave * HD + d) * kMergeLd + lrow] = st.oacc[0][db][i] * fac;
-    }
-  __syncthreads();
-  const int q = tid & 31;
-  const int d0 = (tid >> 5) * 16;
-  float mq = -INFINITY;
-#pragma unroll
-  for (int w = 0; w < 4; ++w) mq = fmaxf(mq, red_m[w * 32 + q]);
-  const float mq_use = (mq == -INFINITY) ? 0.f : mq;
-  float lq = 0.f;
-#pragma unroll
-  for (int w = 0; w < 4; ++w) {
-    const float mw = red_m[w * 32 + q];
-    lq += (mw == -INFINITY) ? 0.f : red_l[w * 32 + q] * __builtin_amdgcn_exp2f(mw - mq_use);
-  }
-  float acc[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    float sum = 0.f;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) sum += ored[(w * HD + d0 + i) * kMergeLd + q];
-    acc[i] = sum;
-  }
-  const int mrow = m_base + q;
-  if (mrow < M) {
-    const int tq = mrow / g;
-    const int hq = hkv * g + (mrow - tq * g);
-    if (a.n_split == 1) {
-      const float inv = lq > 0.f ? 1.f / lq : 0.f;
-      uint16_t* op = a.o + (int64_t)(qrow0 + tq) * a.o_stride + hq * HD + d0;
-      u32x4_t w0, w1;
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        w0[w] = cvt_pk_bf16(acc[2 * w] * inv, acc[2 * w + 1] * inv);
-        w1[w] = cvt_pk_bf16(acc[8 + 2 * w] * inv, acc[8 + 2 * w + 1] * inv);
-      }
-      st128(op, w0);
-      st128(op + 8, w1);
-    } else {
-      const int64_t Prec = (((int64_t)s * a.Hkv + hkv) * a.mtiles + mt) * a.n_split + split;
-      float* po = a.ws + (Prec * 32 + q) * HD + d0;
-#pragma unroll
-      for (int i = 0; i < 16; i += 4) {
-        f32x4_t v4 = {acc[i], acc[i + 1], acc[i + 2], acc[i + 3]};
-        *reinterpret_cast<f32x4_t*>(po + i) = v4;
-      }
-      if (d0 == 0) {  // one writer per row
-        const int64_t nrec = (int64_t)a.n_seg * a.Hkv * a.mtiles * a.n_split;
-        float* pml = a.ws + nrec * 32 * HD + (Prec * 32 + q) * 2;
-        pml[0] = mq;
-        pml[1] = lq;
-      }
-    }
-  }
+  cached_merge_store(a, lds, st, s, hkv, mt, split, qrow0, M, m_base, g);
 }
 
 // Merge the n_split partial records of every (segment, head, M row).
@@ -1054,9 +1071,9 @@ extern "C" int dllm_attn_block_cached_fwd(const dllm_bf16* q, const dllm_bf16* k
   a.logical_blocks = (int)logical;
   a.scale_log2 = softmax_scale * kLog2e;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int nb = (int)((logical + 7) / 8 * 8);
   constexpr int lds_bytes = 2 * CK_STAGE;
   if ((rc = set_lds(attn_cached_kernel, lds_bytes, name))) return rc;
-  const int nb = (int)((logical + 7) / 8 * 8);
   attn_cached_kernel<<<dim3(nb), dim3(256), lds_bytes, st>>>(a);
   if ((rc = check_launch(name))) return rc;
   if (n_split > 1) {

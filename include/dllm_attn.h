@@ -109,7 +109,9 @@ int dllm_attn_varlen_fwd(const dllm_bf16* q, const dllm_bf16* k, const dllm_bf16
  * The cache is [cache_slots, Hkv, D] with slot stride Hkv*D (flat rows, as
  * store_kvcache writes it).  A cached row whose slot is outside
  * [0, cache_slots) is left out of the softmax (the reference would read out
- * of bounds).  max_q bounds the block length of every segment.
+ * of bounds); with cache_slots = 0, k_cache, v_cache and slots may be null
+ * and every cached row is left out.  max_q bounds the block length of every
+ * segment.
  * The work is split over the keys when there are few segments; the partial
  * results go to `workspace`, whose size must be at least
  * dllm_attn_block_cached_workspace_size(...) bytes (0 is valid when that

@@ -180,6 +180,7 @@ def _cached_case(prefix, blk, Hq, Hkv, seed, page=256, extra_pages=3):
     ([2100, 3000, 4096], [32, 32, 32], 32, 32),            # C5-like long prefixes
     ([5, 300], [32, 17], 28, 4),                           # Dream GQA, short block tail
     ([0, 1], [8, 3], 8, 8),                                # empty / single cached row
+    ([2100 + 13 * i for i in range(32)], [32] * 32, 8, 8),  # 256 pairs: one workgroup per pair, no split
 ])
 def test_block_cached(dev, prefix, blk, Hq, Hkv):
     print(f"block_cached prefix={prefix} blk={blk} Hq={Hq} Hkv={Hkv}", flush=True)
@@ -205,6 +206,26 @@ def test_block_cached(dev, prefix, blk, Hq, Hkv):
         r0, r1 = cul[i], cul[i + 1]
         ref = oatt.block_cached(qn[r0:r1], kn[r0:r1], vn[r0:r1], kcn, vcn, slots[i], D ** -0.5, dtype=np.float32)
         assert_attn_close(o[r0:r1], ref, f"seq {i}")
+
+
+@pytest.mark.parametrize("prefix,Hq,Hkv", [([300, 700], 8, 8), ([2100 + 7 * i for i in range(32)], 8, 8)])
+def test_block_cached_without_a_cache(dev, prefix, Hq, Hkv):
+    """cache_slots = 0 (no cache tensor, no slots): every cached row is
+    outside the cache, so the blocks attend to themselves only."""
+    print(f"block_cached without a cache: {len(prefix)} segments", flush=True)
+    D = 128
+    blk = [32] * len(prefix)
+    q, k, v, cu = configs.packed_qkv(blk, Hq, Hkv, D, seed=len(prefix))
+    off = torch.tensor([0] + np.cumsum(prefix).tolist(), dtype=torch.int32, device=dev)
+    max_keys = max(prefix) + 32
+    ws_b = _capi.block_cached_workspace_size(len(blk), 32, max_keys, Hq, Hkv, D)
+    ws = torch.empty(max(ws_b, 16), dtype=torch.uint8, device=dev) if ws_b else None
+    o = torch.zeros(q.shape, dtype=torch.bfloat16, device=dev)
+    _capi.attn_block_cached_fwd(q.to(dev), k.to(dev), v.to(dev), o, cu.to(dev), None, len(blk), 32, max_keys,
+                                None, None, None, off, D ** -0.5, ws)
+    torch.cuda.synchronize()
+    ref = oatt.varlen(to_np(q), to_np(k), to_np(v), cu.numpy(), cu.numpy(), D ** -0.5, dtype=np.float32)
+    assert_attn_close(o, ref, "blocks only")
 
 
 def test_block_cached_invalid_slots_are_excluded(dev):

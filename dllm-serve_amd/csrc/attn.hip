@@ -79,9 +79,6 @@ __device__ __forceinline__ u32x4_t bload(__amdgpu_buffer_rsrc_t r, uint32_t voff
 // below 2^kLazy, well inside the bf16 / fp32 range.
 constexpr float kLazy = 8.0f;
 
-// Partial accumulators per S^T block (see dense_tile).
-constexpr int kSSplit = 2;
-
 // ---------------------------------------------------------------------------
 // K3a, dense varlen attention: K and V tiles go HBM -> LDS by buffer DMA
 // (buffer_load_dwordx4 ... lds, no VGPR staging); the V^T MFMA operand is
@@ -146,18 +143,38 @@ __device__ __forceinline__ void dense_addr(DenseAddr& ad, int lane, uint32_t kS,
 }
 
 // Softmax state of NQ query blocks (32 M rows each) of one wavefront.
+// thr = m_run + kLazy and neg_m = -m_run (0 while m_run is -inf) change only
+// when m_run does, so the per-tile test and exponent need no extra VALU work.
 template <int NQ>
 struct DenseState {
   f32x16_t oacc[NQ][4];
   float m_run[NQ];
   float l_run[NQ];
+  float thr[NQ];
+  float neg_m[NQ];
 };
+
+template <int NQ>
+__device__ __forceinline__ void dense_state_init(DenseState<NQ>& st) {
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) st.oacc[q][db][i] = 0.f;
+    st.m_run[q] = -INFINITY;
+    st.l_run[q] = 0.f;
+    st.thr[q] = -INFINITY;
+    st.neg_m[q] = 0.f;
+  }
+}
 
 // Online-softmax update of one query block from its two S^T key blocks;
 // returns the packed P^T fragments (B operands of O^T += V^T P^T).
 template <int KB, bool MASK>
 __device__ __forceinline__ void dense_softmax(f32x16_t (&sacc)[KB], f32x16_t (&oacc)[4], float& m_run, float& l_run,
-                                              bf16x8_t (&pf)[2 * KB], float c, int k_valid, uint64_t bad, int hl) {
+                                              float& thr, float& neg_m, bf16x8_t (&pf)[2 * KB], float c, int k_valid,
+                                              uint64_t bad, int hl) {
   float mx = -INFINITY;
 #pragma unroll
   for (int b = 0; b < KB; ++b)
@@ -170,7 +187,7 @@ __device__ __forceinline__ void dense_softmax(f32x16_t (&sacc)[KB], f32x16_t (&o
       mx = fmaxf(mx, sacc[b][i]);
     }
   mx = pair_max32(mx) * c;
-  const bool need = mx > m_run + kLazy;
+  const bool need = mx > thr;
   if (__builtin_amdgcn_ballot_w64(need)) {
     const float m_new = need ? mx : m_run;
     const float alpha = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
@@ -180,8 +197,9 @@ __device__ __forceinline__ void dense_softmax(f32x16_t (&sacc)[KB], f32x16_t (&o
 #pragma unroll
       for (int i = 0; i < 16; ++i) oacc[db][i] *= alpha;
     m_run = m_new;
+    thr = m_run + kLazy;
+    neg_m = (m_run == -INFINITY) ? 0.f : -m_run;
   }
-  const float neg_m = (m_run == -INFINITY) ? 0.f : -m_run;
   // The row sum adds the bf16-rounded numerators, the same values the O^T
   // product consumes; two partial sums keep the dependent chain short.
   float psum[2] = {0.f, 0.f};
@@ -249,23 +267,19 @@ __device__ __forceinline__ void dense_tile(const uint8_t* Ks, const uint8_t* Vs,
   const int lane = threadIdx.x & 63;
   const int hl = lane >> 5;
   // kk outer, key block inner: the KB*NQ accumulators form independent MFMA
-  // chains that interleave instead of one chain waiting on itself.
-  // Each S^T block's head-dim reduction is split over SPLIT partial
-  // accumulators (kk % SPLIT) so KB*NQ*SPLIT independent MFMA chains are in
-  // flight: a dependent 32x32x16 MFMA waits for its predecessor, and a
-  // single chain per wavefront leaves the matrix pipe idle.
-  // 64-key tiles already give two independent S^T chains (one per 32-key
-  // block), so their reduction is not split (1.5-2 % faster at 2 x 4096).
-  constexpr int SPLIT = TK == 32 ? kSSplit : 1;
-  f32x16_t sp[NQ][KB][SPLIT];
+  // chains that interleave instead of one chain waiting on itself.  Each
+  // S^T block is one chain over the head dimension: the wavefronts sharing
+  // a SIMD interleave their chains, and splitting the reduction over two
+  // partial accumulators (to lengthen the chain count) costs 16 VALU adds per
+  // tile to merge them -- 2-5 % slower at every measured shape, since the
+  // softmax VALU work rivals the MFMA work.
+  f32x16_t sacc[NQ][KB];
 #pragma unroll
   for (int q = 0; q < NQ; ++q)
 #pragma unroll
     for (int b = 0; b < KB; ++b)
 #pragma unroll
-      for (int h = 0; h < SPLIT; ++h)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) sp[q][b][h][i] = 0.f;
+      for (int i = 0; i < 16; ++i) sacc[q][b][i] = 0.f;
 #pragma unroll
   for (int kk = 0; kk < 8; ++kk) {
 #pragma unroll
@@ -274,22 +288,14 @@ __device__ __forceinline__ void dense_tile(const uint8_t* Ks, const uint8_t* Vs,
           as_bf16x8(*reinterpret_cast<const u32x4_t*>(Ks + b * 32 * 256 + (ad.kbase ^ (uint32_t)(32 * kk))));
 #pragma unroll
       for (int q = 0; q < NQ; ++q)
-        sp[q][b][kk % SPLIT] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, qf[q][kk], sp[q][b][kk % SPLIT], 0, 0, 0);
+        sacc[q][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, qf[q][kk], sacc[q][b], 0, 0, 0);
     }
   }
-  f32x16_t sacc[NQ][KB];
-#pragma unroll
-  for (int q = 0; q < NQ; ++q)
-#pragma unroll
-    for (int b = 0; b < KB; ++b) {
-      sacc[q][b] = sp[q][b][0];
-#pragma unroll
-      for (int h = 1; h < SPLIT; ++h) sacc[q][b] += sp[q][b][h];
-    }
   bf16x8_t pf[NQ][2 * KB];
 #pragma unroll
   for (int q = 0; q < NQ; ++q)
-    dense_softmax<KB, MASK>(sacc[q], st.oacc[q], st.m_run[q], st.l_run[q], pf[q], c, k_valid, bad, hl);
+    dense_softmax<KB, MASK>(sacc[q], st.oacc[q], st.m_run[q], st.l_run[q], st.thr[q], st.neg_m[q], pf[q], c, k_valid,
+                            bad, hl);
   if constexpr (UNTRACKED_V) {
     static_assert(KB == 1, "one 32-key block per call");
     u32x2_t r[16];
@@ -447,15 +453,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(OCC, OC
   }
 
   DenseState<NQ> st;
-#pragma unroll
-  for (int q = 0; q < NQ; ++q) {
-#pragma unroll
-    for (int db = 0; db < 4; ++db)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) st.oacc[q][db][i] = 0.f;
-    st.m_run[q] = -INFINITY;
-    st.l_run[q] = 0.f;
-  }
+  dense_state_init(st);
   const float c = a.scale_log2;
 
   // Full tiles, the next tile's DMA in flight; the last tile is peeled off
@@ -803,12 +801,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   DenseAddr ad;
   dense_addr(ad, lane, 0u, 0u);
   DenseState<1> st;
-#pragma unroll
-  for (int db = 0; db < 4; ++db)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) st.oacc[0][db][i] = 0.f;
-  st.m_run[0] = -INFINITY;
-  st.l_run[0] = 0.f;
+  dense_state_init(st);
   const float c = a.scale_log2;
 
   for (int t = 0; t < ntiles; ++t) {

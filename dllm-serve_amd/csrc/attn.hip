@@ -201,8 +201,9 @@ __device__ __forceinline__ void dense_softmax(f32x16_t (&sacc)[KB], f32x16_t (&o
     neg_m = (m_run == -INFINITY) ? 0.f : -m_run;
   }
   // The row sum adds the bf16-rounded numerators, the same values the O^T
-  // product consumes; two partial sums keep the dependent chain short.
-  float psum[2] = {0.f, 0.f};
+  // product consumes; two partial sums (one starting from l_run) keep the
+  // dependent chain short.
+  float psum[2] = {l_run, 0.f};
 #pragma unroll
   for (int b = 0; b < KB; ++b)
 #pragma unroll
@@ -217,7 +218,7 @@ __device__ __forceinline__ void dense_softmax(f32x16_t (&sacc)[KB], f32x16_t (&o
       }
       pf[2 * b + j] = as_bf16x8(pk);
     }
-  l_run += psum[0] + psum[1];
+  l_run = psum[0] + psum[1];
 }
 
 // One key tile (TK keys) for one wavefront owning NQ query blocks: every K
@@ -367,21 +368,25 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(OCC, OC
   const int hl = lane >> 5;
 
   const uint32_t kS = (uint32_t)(a.k_stride * 2), vS = (uint32_t)(a.v_stride * 2);
-  const __amdgpu_buffer_rsrc_t krs =
-      make_rsrc(a.k + (int64_t)krow0 * a.k_stride + hkv * HD, Lk > 0 ? (uint32_t)(Lk - 1) * kS + HD * 2 : 0u);
-  const __amdgpu_buffer_rsrc_t vrs =
-      make_rsrc(a.v + (int64_t)krow0 * a.v_stride + hkv * HD, Lk > 0 ? (uint32_t)(Lk - 1) * vS + HD * 2 : 0u);
+  const uint16_t* kseg = a.k + (int64_t)krow0 * a.k_stride + hkv * HD;
+  const uint16_t* vseg = a.v + (int64_t)krow0 * a.v_stride + hkv * HD;
   DenseAddr ad;
   dense_addr(ad, lane, kS, vS);
 
   // DMA instruction j (global index q = DMA_PER_WAVE*wave + j, or q = wave
   // when there are more wavefronts than instructions) covers tile rows 4q..4q+3.
+  // Each tile gets buffer resources based at its first row (scalar work), so
+  // the per-lane offsets are the same for every tile and no VALU work is
+  // spent per tile; rows past the segment's last still read as zero.
   auto issue = [&](uint8_t* stage, int k0) {
+    const uint32_t rows_left = (uint32_t)(Lk - 1 - k0);  // k0 < Lk: only tiles that exist are issued
+    const __amdgpu_buffer_rsrc_t krs = make_rsrc(kseg + (int64_t)k0 * a.k_stride, rows_left * kS + HD * 2);
+    const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vseg + (int64_t)k0 * a.v_stride, rows_left * vS + HD * 2);
 #pragma unroll
     for (int j = 0; j < DMA_PER_WAVE; ++j) {
       const int q = NW > NDMA ? wave : DMA_PER_WAVE * wave + j;
       if (q >= NDMA) break;  // wave-uniform
-      const uint32_t row = (uint32_t)(k0 + 4 * q);
+      const uint32_t row = (uint32_t)(4 * q);
       dma16(krs, stage + q * 1024, row * kS + (ad.kdma ^ (uint32_t)(64 * (q & 3))));
       dma16(vrs, stage + TK * 256 + q * 1024, row * vS + ad.vdma);
     }

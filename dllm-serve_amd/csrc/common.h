@@ -65,10 +65,15 @@ __device__ __forceinline__ float add_bf16x2(uint32_t pk, float acc) {
 // Combine a value across the lane pair (l, l ^ 32) with v_permlane32_swap
 // (gfx950): after the swap one operand holds lanes 0..31 of x in both halves
 // and the other lanes 32..63.  Every lane of the wavefront must be active.
+// pair_max32 takes the maximum with one v_max_f32: fmaxf on the swap's
+// outputs would first quieten both operands (two more VALU instructions),
+// which the callers' NaN-free inputs never need.
 __device__ __forceinline__ float pair_max32(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x),
                                                   false, false);
-  return fmaxf(__builtin_bit_cast(float, (uint32_t)r[0]), __builtin_bit_cast(float, (uint32_t)r[1]));
+  float m;
+  asm("v_max_f32 %0, %1, %2" : "=v"(m) : "v"((uint32_t)r[0]), "v"((uint32_t)r[1]));
+  return m;
 }
 __device__ __forceinline__ float pair_sum32(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x),

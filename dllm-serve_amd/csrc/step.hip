@@ -84,6 +84,7 @@ __global__ __launch_bounds__(1024) void step_build_kernel(StepBuildArgs a) {
   __shared__ int s_rows[kStepMaxSeq], s_start[kStepMaxSeq], s_cu[kStepMaxSeq];
   __shared__ int s_keep[kStepMaxSeq], s_sbase[kStepMaxSeq], s_pages[kStepMaxSeq];
   __shared__ int s_wlo[kStepMaxSeq], s_wn[kStepMaxSeq], s_woff[kStepMaxSeq];
+  __shared__ int s_dense_rows[kStepMaxSeq];  // rows of a full-attention sequence, -1 otherwise
   __shared__ int s_scan[16];
   const int i = threadIdx.x;
   const bool live = i < a.n;
@@ -138,7 +139,7 @@ __global__ __launch_bounds__(1024) void step_build_kernel(StepBuildArgs a) {
   }
   int tot_rows, n_dense, n_cached, n_job, tot_cached_keep, tot_job_keep, tot_win, any_err;
   const int cu0 = block_exscan(rows, s_scan, &tot_rows);
-  const int d_at = block_exscan(live && (mode == 0 || mode == 1), s_scan, &n_dense);
+  block_exscan(live && (mode == 0 || mode == 1), s_scan, &n_dense);
   const int c_at = block_exscan(live && mode == 2, s_scan, &n_cached);
   const int j_at = block_exscan(live && mode == 1, s_scan, &n_job);
   const int ck = block_exscan(mode == 2 ? keep : 0, s_scan, &tot_cached_keep);
@@ -160,7 +161,7 @@ __global__ __launch_bounds__(1024) void step_build_kernel(StepBuildArgs a) {
     s_wn[i] = wn;
     s_woff[i] = woff;
     a.cu[i] = cu0;
-    if (mode == 0 || mode == 1) a.dense_ids[d_at] = i;
+    s_dense_rows[i] = (mode == 0 || mode == 1) ? rows : -1;
     if (mode == 2) {
       a.cached_ids[c_at] = i;
       a.slot_off[c_at] = sbase;
@@ -198,6 +199,16 @@ __global__ __launch_bounds__(1024) void step_build_kernel(StepBuildArgs a) {
     a.counts[7] = any_err;
   }
   __syncthreads();
+  // full-attention sequences longest first, ties by index (the host's order)
+  if (live && s_dense_rows[i] >= 0) {
+    const int ri = s_dense_rows[i];
+    int rank = 0;
+    for (int j = 0; j < a.n; ++j) {
+      const int rj = s_dense_rows[j];
+      rank += (rj > ri || (rj == ri && j < i)) ? 1 : 0;
+    }
+    a.dense_ids[rank] = i;
+  }
   if (!fits) return;  // uniform: the host sizes the buffers from the same state
   for (int q = 0; q < a.n; ++q) {
     const int r0 = s_cu[q], nr = s_rows[q], st = s_start[q];

@@ -128,7 +128,10 @@ class StepLayout:
         self.cu = np.zeros(self.n_seq + 1, dtype=np.int64)
         self.cu[1:] = np.cumsum(rows)
         self.any_skipped = any(m == -1 for m in modes)
-        self.dense = [i for i, m in enumerate(modes) if m in (0, 1)]
+        # longest first (ties by index): with the XCD interleave of the dense
+        # kernel, long segments then start early and short ones fill the tail
+        # (16 ragged Dream GQA segments: 3-12 % faster than batch order)
+        self.dense = sorted((i for i, m in enumerate(modes) if m in (0, 1)), key=lambda i: (-rows[i], i))
         self.jobs_idx = [i for i, m in enumerate(modes) if m == 1]
         self.cached = [i for i, m in enumerate(modes) if m == 2]
         self.n_dense = len(self.dense)

@@ -270,7 +270,8 @@ int dllm_lowconf_unmask(int64_t* tokens, int64_t n_tokens, const int32_t* seq_pa
  * describes (n = n_seq):
  *   cu [n+1]            packed row offsets of the fed rows (all N rows; only
  *                       the block's rows in cache state 2)
- *   dense_ids [max(1,n)]  sequences of full attention (state 0/1 or none), in order
+ *   dense_ids [max(1,n)]  sequences of full attention (state 0/1 or none), most rows
+ *                        first (ties by index)
  *   cached_ids [max(1,n)] sequences in state 2, in order
  *   slot_off [n+1]      their slot ranges in `slots`
  *   jobs [max(1,n)][6]  state-1 selection jobs {row0, n_tok, blk_start,

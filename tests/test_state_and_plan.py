@@ -110,7 +110,8 @@ def test_step_plan_tables():
     plan = StepPlan(ctx, torch.device("cpu"), 32, 128, 32)
     assert plan.total_rows == 164 + 32 + 214
     assert plan.cu.tolist() == [0, 164, 196, 410]
-    assert plan.n_dense == 2 and plan.dense_ids.tolist() == [0, 2] and plan.max_q_dense == 214
+    # dense segments longest first: C (214 rows) before A (164)
+    assert plan.n_dense == 2 and plan.dense_ids.tolist() == [2, 0] and plan.max_q_dense == 214
     assert plan.n_cached == 1 and plan.cached_ids.tolist() == [1]
     n_b = keep_count(264 - 32, 0.5)   # 116
     n_c = keep_count(214 - 32, 0.5)   # 91

@@ -137,7 +137,8 @@ def bench_dense(lens, Hq, Hkv, D, n_layers, steps, warmup, dev, seed=0):
     ms_step = time_layer_calls(attn, layers, steps, warmup)
     flops_call = attention_flops(lens, lens, Hq, D)
     bytes_call = attention_bytes(lens, lens, Hq, Hkv, D)
-    # per-launch kernel time: the raw varlen kernel over distinct layers' buffers
+    # per-launch kernel time: the raw varlen kernel over distinct layers' buffers,
+    # with the step plan's segment order (longest first), as the layer calls run it
     plan = get_context()._dllm_plan
     outs = [torch.empty_like(q) for q, _, _ in layers]
     state = {"i": 0}
@@ -146,7 +147,8 @@ def bench_dense(lens, Hq, Hkv, D, n_layers, steps, warmup, dev, seed=0):
         i = state["i"] % n_layers
         state["i"] += 1
         q, k, v = layers[i]
-        _capi.attn_varlen_fwd(q, k, v, outs[i], plan.cu, plan.cu, None, len(lens), max(lens), D ** -0.5)
+        _capi.attn_varlen_fwd(q, k, v, outs[i], plan.cu, plan.cu, plan.dense_ids, plan.n_dense, plan.max_q_dense,
+                              D ** -0.5)
 
     ms_kernel = time_kernel(one, iters=4 * n_layers)
     # the same step's layer calls captured once in a HIP graph and replayed

@@ -62,8 +62,8 @@ struct AttnArgs {
 // one contiguous eighth instead left ragged batches unbalanced: with 16
 // segments of 410..1245 tokens the busiest XCD held 1.6x the mean work
 // (those 16 segments, 28 query / 4 KV heads: 226 -> 172 us with chunks of
-// 4).  The grid must be a
-// multiple of 8 * ch; the map is then a bijection onto [0, grid).
+// 4).  The grid must be a multiple of 8 * ch; the map is then a bijection
+// onto [0, grid).
 __device__ __forceinline__ int xcd_remap(int b, int ch) {
   const int x = b & 7, i = b >> 3;
   const int j = i / ch;

@@ -228,6 +228,54 @@ def test_block_cached_without_a_cache(dev, prefix, Hq, Hkv):
     assert_attn_close(o, ref, "blocks only")
 
 
+@pytest.mark.parametrize("lens,Hq,Hkv", [
+    ([333, 20, 517], 28, 4),     # 4-wavefront launch: 29 m-tiles, chunks of 16, 348 blocks in a grid of 384
+    ([300] * 5, 32, 32),         # 12-wavefront launch: 160 pairs, chunks of 1, grid 160
+    ([2500, 100], 8, 2),         # 8-wavefront launch: 40 m-tiles, chunks of 16, 160 blocks in a grid of 256
+    ([129, 5, 131], 8, 8),       # 4-wavefront launch: 2 m-tiles, chunks of 2, 48 blocks in a grid of 48
+])
+def test_varlen_xcd_interleave_covers_every_block(dev, lens, Hq, Hkv):
+    """Logical blocks are dealt to the XCDs in chunks and the grid is padded
+    to a multiple of 8 chunks: every output row is written (none left at the
+    NaN fill) and matches the oracle."""
+    print(f"varlen xcd interleave lens={lens} Hq={Hq} Hkv={Hkv}", flush=True)
+    q, k, v, cu = configs.packed_qkv(lens, Hq, Hkv, 128, seed=7 + sum(lens))
+    o = _run_varlen(q, k, v, cu, dev, o_init=torch.full(q.shape, float("nan"), dtype=torch.bfloat16))
+    assert not torch.isnan(o).any(), "rows left unwritten"
+    ref = oatt.varlen(to_np(q), to_np(k), to_np(v), cu.numpy(), cu.numpy(), 128 ** -0.5, dtype=np.float32)
+    assert_attn_close(o, ref, f"lens={lens}")
+
+
+def test_block_cached_xcd_interleave_covers_every_block(dev):
+    """Key-split launch (chunks of n_split x m-tiles, padded grid): every row
+    written and equal to the oracle."""
+    prefix, blk, Hq, Hkv = [1000, 37, 650], [20, 20, 9], 28, 4
+    print(f"block_cached xcd interleave prefix={prefix}", flush=True)
+    q, k, v, cu, kc, vc, slots = _cached_case(prefix, blk, Hq, Hkv, seed=11)
+    D = 128
+    slot_off = [0]
+    for s_ in slots:
+        slot_off.append(slot_off[-1] + len(s_))
+    flat_slots = torch.tensor([x for s_ in slots for x in s_], dtype=torch.int32)
+    o = torch.full(q.shape, float("nan"), dtype=torch.bfloat16, device=dev)
+    max_keys = max(p + b for p, b in zip(prefix, blk))
+    ws_bytes = _capi.block_cached_workspace_size(len(blk), max(blk), max_keys, Hq, Hkv, D)
+    assert ws_bytes > 0, "this shape is meant to split the keys"
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    _capi.attn_block_cached_fwd(q.to(dev), k.to(dev), v.to(dev), o, cu.to(dev), None, len(blk), max(blk), max_keys,
+                                kc.to(dev), vc.to(dev), flat_slots.to(dev),
+                                torch.tensor(slot_off, dtype=torch.int32, device=dev), D ** -0.5, ws)
+    torch.cuda.synchronize()
+    assert not torch.isnan(o).any(), "rows left unwritten"
+    kcn, vcn = to_np(kc), to_np(vc)
+    cul = cu.tolist()
+    qn, kn, vn = to_np(q), to_np(k), to_np(v)
+    for i in range(len(blk)):
+        r0, r1 = cul[i], cul[i + 1]
+        ref = oatt.block_cached(qn[r0:r1], kn[r0:r1], vn[r0:r1], kcn, vcn, slots[i], D ** -0.5, dtype=np.float32)
+        assert_attn_close(o[r0:r1], ref, f"seq {i}")
+
+
 def test_block_cached_invalid_slots_are_excluded(dev):
     """Slots outside the cache are left out of the softmax."""
     print("block_cached invalid slots", flush=True)

@@ -118,8 +118,11 @@ __device__ __forceinline__ void vm_wait() {
   asm volatile("" ::: "memory");
 }
 
+// AUX = 2: non-temporal (streaming) policy, for bytes that one workgroup reads once.
+template <int AUX = 0>
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint8_t* lds_dst, uint32_t voff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_dst, 16, (int)voff, 0, 0, 0);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_dst, 16, (int)voff, 0, 0,
+                                           AUX);
 }
 
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
@@ -351,6 +354,11 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(OCC, OC
   static_assert(TK % 32 == 0, "tile shape");
   static_assert(NDMA % NW == 0 || (NW > NDMA && ST == 2), "an uneven DMA split needs the full wait of two stages");
   constexpr bool QDMA = NQ == 1 && NW == 4 * OCC;  // one workgroup per CU
+  // The 12-wavefront launch runs one workgroup per (segment, KV head) pair,
+  // so its K/V bytes, like every launch's Q rows, are read once: streaming
+  // loads for them (C2 step 27.7 -> 27.2 us).  The other launches share a
+  // pair's K/V between the workgroups of its m-tiles and keep the default.
+  constexpr int KV_AUX = NW == 12 ? kStreamAux : 0;
   constexpr int QOFF = ST * STAGE;                 // Q rows after the K/V stages (NW * 8 KiB)
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int L = xcd_remap(blockIdx.x, a.xcd_chunk);
@@ -396,8 +404,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(OCC, OC
       const int q = NW > NDMA ? wave : DMA_PER_WAVE * wave + j;
       if (q >= NDMA) break;  // wave-uniform
       const uint32_t row = (uint32_t)(4 * q);
-      dma16(krs, stage + q * 1024, row * kS + (ad.kdma ^ (uint32_t)(64 * (q & 3))));
-      dma16(vrs, stage + TK * 256 + q * 1024, row * vS + ad.vdma);
+      dma16<KV_AUX>(krs, stage + q * 1024, row * kS + (ad.kdma ^ (uint32_t)(64 * (q & 3))));
+      dma16<KV_AUX>(vrs, stage + TK * 256 + q * 1024, row * vS + ad.vdma);
     }
   };
 
@@ -433,7 +441,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(OCC, OC
                                  ? (uint32_t)tok * qS + (uint32_t)((hkv * g + rem) * HD * 2) +
                                        (uint32_t)((P ^ (R & 15)) * 16)
                                  : qbytes;
-        dma16(qrs, qdst + j * 1024, off);
+        dma16<kStreamAux>(qrs, qdst + j * 1024, off);
         tok += q4;
         rem += r4;
         if (rem >= g) {

@@ -27,6 +27,7 @@
 
 #include <math.h>
 
+#include <mutex>
 #include <type_traits>
 
 namespace dllm {
@@ -1047,14 +1048,12 @@ extern "C" size_t dllm_attn_block_cached_workspace_size(int n_seg, int max_q, in
   return nrec * 32 * (HD + 2) * sizeof(float);
 }
 
-extern "C" int dllm_attn_block_cached_fwd(const dllm_bf16* q, const dllm_bf16* k, const dllm_bf16* v, dllm_bf16* o,
-                                          const int32_t* cu, const int32_t* seg_ids, int n_seg, int max_q,
-                                          int max_keys, const dllm_bf16* k_cache, const dllm_bf16* v_cache,
-                                          int64_t cache_slots, const int32_t* slots, const int32_t* slot_off,
-                                          int Hq, int Hkv, int D, int64_t q_stride_tok, int64_t k_stride_tok,
-                                          int64_t v_stride_tok, int64_t o_stride_tok, float softmax_scale,
-                                          void* workspace, size_t workspace_bytes, void* stream) {
-  const char* name = "dllm_attn_block_cached_fwd";
+static int block_cached_impl(const char* name, const dllm_bf16* q, const dllm_bf16* k, const dllm_bf16* v,
+                             dllm_bf16* o, const int32_t* cu, const int32_t* seg_ids, int n_seg, int max_q,
+                             int max_keys, const dllm_bf16* k_cache, const dllm_bf16* v_cache, int64_t cache_slots,
+                             const int32_t* slots, const int32_t* slot_off, int Hq, int Hkv, int D,
+                             int64_t q_stride_tok, int64_t k_stride_tok, int64_t v_stride_tok, int64_t o_stride_tok,
+                             float softmax_scale, void* workspace, size_t workspace_bytes, void* stream) {
   int rc = common_checks(name, q, k, v, o, Hq, Hkv, D, q_stride_tok, k_stride_tok, v_stride_tok, o_stride_tok);
   if (rc) return rc;
   if (n_seg < 0 || max_q < 0 || max_keys < 0) return fail(DLLM_ERR_INVALID_ARG, "%s: negative size", name);
@@ -1106,4 +1105,74 @@ extern "C" int dllm_attn_block_cached_fwd(const dllm_bf16* q, const dllm_bf16* k
     if ((rc = check_launch(name))) return rc;
   }
   return DLLM_OK;
+}
+
+extern "C" int dllm_attn_block_cached_fwd(const dllm_bf16* q, const dllm_bf16* k, const dllm_bf16* v, dllm_bf16* o,
+                                          const int32_t* cu, const int32_t* seg_ids, int n_seg, int max_q,
+                                          int max_keys, const dllm_bf16* k_cache, const dllm_bf16* v_cache,
+                                          int64_t cache_slots, const int32_t* slots, const int32_t* slot_off,
+                                          int Hq, int Hkv, int D, int64_t q_stride_tok, int64_t k_stride_tok,
+                                          int64_t v_stride_tok, int64_t o_stride_tok, float softmax_scale,
+                                          void* workspace, size_t workspace_bytes, void* stream) {
+  return block_cached_impl("dllm_attn_block_cached_fwd", q, k, v, o, cu, seg_ids, n_seg, max_q, max_keys, k_cache,
+                           v_cache, cache_slots, slots, slot_off, Hq, Hkv, D, q_stride_tok, k_stride_tok,
+                           v_stride_tok, o_stride_tok, softmax_scale, workspace, workspace_bytes, stream);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free variant: the split partials go to `scratch`, a file-scope
+// device array (one copy per GPU, held until the process ends), instead of
+// a caller workspace.  In host code `scratch` names a host-side stand-in, not
+// device memory: its device address is looked up once per device with
+// hipGetSymbolAddress (with that device current) and only that address is
+// ever handed to kernels.  The partial records are written in full by the
+// splits before the combine kernel reads them, so nothing needs clearing
+// between calls; calls that overlap on one GPU share the array and race.
+constexpr size_t kScratchBytes = (size_t)16 << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxDevices];
+
+// Device address of `scratch` on the current device (looked up on first use).
+static int scratch_ptr(const char* name, void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(DLLM_ERR_HIP, "%s: hipGetDevice: %s", name, hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(DLLM_ERR_UNSUPPORTED, "%s: device %d beyond %d", name, dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(DLLM_ERR_HIP, "%s: hipGetSymbolAddress(scratch): %s", name, hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return DLLM_OK;
+}
+
+extern "C" size_t dllm_attn_block_cached_noalloc_max_workspace(void) { return kScratchBytes; }
+
+extern "C" int dllm_attn_block_cached_fwd_noalloc(const dllm_bf16* q, const dllm_bf16* k, const dllm_bf16* v,
+                                                  dllm_bf16* o, const int32_t* cu, const int32_t* seg_ids,
+                                                  int n_seg, int max_q, int max_keys, const dllm_bf16* k_cache,
+                                                  const dllm_bf16* v_cache, int64_t cache_slots, const int32_t* slots,
+                                                  const int32_t* slot_off, int Hq, int Hkv, int D,
+                                                  int64_t q_stride_tok, int64_t k_stride_tok, int64_t v_stride_tok,
+                                                  int64_t o_stride_tok, float softmax_scale, void* stream) {
+  const char* name = "dllm_attn_block_cached_fwd_noalloc";
+  const size_t need = dllm_attn_block_cached_workspace_size(n_seg, max_q, max_keys, Hq, Hkv, D);
+  if (need > kScratchBytes)
+    return fail(DLLM_ERR_UNSUPPORTED, "%s: this launch needs %zu bytes of split partials, beyond the %zu-byte static scratch",
+                name, need, kScratchBytes);
+  void* ws = nullptr;
+  if (need > 0) {
+    int rc = scratch_ptr(name, &ws);
+    if (rc) return rc;
+  }
+  return block_cached_impl(name, q, k, v, o, cu, seg_ids, n_seg, max_q, max_keys, k_cache, v_cache, cache_slots,
+                           slots, slot_off, Hq, Hkv, D, q_stride_tok, k_stride_tok, v_stride_tok, o_stride_tok,
+                           softmax_scale, ws, need > 0 ? kScratchBytes : 0, stream);
 }

@@ -45,6 +45,12 @@ SIGNATURES = {
         [_P, _P, _P, _P, _P, _P, _I, _I, _I, _P, _P, _I64, _P, _P, _I, _I, _I,
          _I64, _I64, _I64, _I64, _F, _P, _SZ, _P],
     ),
+    "dllm_attn_block_cached_noalloc_max_workspace": (_SZ, []),
+    "dllm_attn_block_cached_fwd_noalloc": (
+        _I,
+        [_P, _P, _P, _P, _P, _P, _I, _I, _I, _P, _P, _I64, _P, _P, _I, _I, _I,
+         _I64, _I64, _I64, _I64, _F, _P],
+    ),
     "dllm_select_kv_workspace_size": (_SZ, [_I, _I, _I, _I, _I, _I]),
     "dllm_select_kv_store": (
         _I,
@@ -168,6 +174,28 @@ def attn_block_cached_fwd(q, k, v, o, cu, seg_ids, n_seg, max_q, max_keys,
         q.stride(0), k.stride(0), v.stride(0), o.stride(0), float(scale),
         _ptr(workspace), ws_bytes, _stream(q.device))
     _check(rc, "dllm_attn_block_cached_fwd")
+
+
+def block_cached_noalloc_max_workspace() -> int:
+    return int(load().dllm_attn_block_cached_noalloc_max_workspace())
+
+
+def attn_block_cached_fwd_noalloc(q, k, v, o, cu, seg_ids, n_seg, max_q, max_keys,
+                                  k_cache, v_cache, slots, slot_off, scale):
+    """K3b with its split partials in the library's static device scratch
+    (allocates nothing; calls that overlap on one GPU race)."""
+    _require_gpu(q, k, v, o, cu, slot_off)
+    lib = load()
+    Hkv, D = k.shape[1], k.shape[2]
+    cache_slots = k_cache.numel() // (Hkv * D) if k_cache is not None and k_cache.numel() else 0
+    rc = lib.dllm_attn_block_cached_fwd_noalloc(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+        cu.data_ptr(), _ptr(seg_ids), n_seg, max_q, max_keys,
+        _ptr(k_cache) if cache_slots else None, _ptr(v_cache) if cache_slots else None,
+        cache_slots, _ptr(slots) if cache_slots else None, slot_off.data_ptr(),
+        q.shape[1], Hkv, D,
+        q.stride(0), k.stride(0), v.stride(0), o.stride(0), float(scale), _stream(q.device))
+    _check(rc, "dllm_attn_block_cached_fwd_noalloc")
 
 
 def select_workspace_size(n_job, max_kc, Hq, Hkv, D, head_select) -> int:

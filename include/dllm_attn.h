@@ -128,6 +128,28 @@ int dllm_attn_block_cached_fwd(const dllm_bf16* q, const dllm_bf16* k, const dll
                                void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * K3b without a caller workspace.  No counterpart in the reference: this is
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid allocation).  Same
+ * arguments, kernels and results as dllm_attn_block_cached_fwd, but the split
+ * partials go to a static device array of the library (one per GPU, held
+ * until the process ends) of dllm_attn_block_cached_noalloc_max_workspace()
+ * bytes (16 MiB); a launch whose dllm_attn_block_cached_workspace_size(...)
+ * exceeds it fails with DLLM_ERR_UNSUPPORTED and launches nothing.  The call
+ * allocates nothing.  Every call on one GPU shares that array: calls that
+ * overlap on one GPU (different streams, or host threads) race and must be
+ * serialised by the caller.
+ */
+size_t dllm_attn_block_cached_noalloc_max_workspace(void);
+int dllm_attn_block_cached_fwd_noalloc(const dllm_bf16* q, const dllm_bf16* k, const dllm_bf16* v, dllm_bf16* o,
+                                       const int32_t* cu, const int32_t* seg_ids, int n_seg, int max_q,
+                                       int max_keys, const dllm_bf16* k_cache, const dllm_bf16* v_cache,
+                                       int64_t cache_slots, const int32_t* slots, const int32_t* slot_off,
+                                       int Hq, int Hkv, int D,
+                                       int64_t q_stride_tok, int64_t k_stride_tok, int64_t v_stride_tok,
+                                       int64_t o_stride_tok, float softmax_scale, void* stream);
+
+/*
  * K5 / K6 -- sparse KV selection fused with the KV-cache scatter (mode 1 /
  * "compute cache").  Replaces _select_important_head_kv (head_select != 0,
  * dllmserve/layers/attention.py:344-413), _select_important_kv (head_select

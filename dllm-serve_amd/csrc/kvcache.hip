@@ -132,7 +132,7 @@ static int kv_copy(const uint16_t* sk, const uint16_t* sv, uint16_t* dk, uint16_
 
 extern "C" const char* dllm_last_error(void) { return dllm::g_err; }
 
-extern "C" int dllm_abi_version(void) { return 103; }
+extern "C" int dllm_abi_version(void) { return 200; }
 
 extern "C" int dllm_store_kvcache(const dllm_bf16* key, int64_t key_stride_tok, const dllm_bf16* value,
                                   int64_t value_stride_tok, dllm_bf16* k_cache, dllm_bf16* v_cache,

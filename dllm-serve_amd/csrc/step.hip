@@ -25,7 +25,9 @@
 namespace dllm {
 
 constexpr int kStepMaxSeq = 1024;
-constexpr int kStateCols = 10;  // P, N, sparse, block_len, block_idx, step_in_block, cache_state, delay, steps, cur
+// P, N, sparse, block_len, block_idx, step_in_block, cache_state, delay, steps, cur, head_select, pool_k
+constexpr int kStateCols = 12;
+constexpr int kJobCols = 8;  // row0, n_tok, blk_start, blk_len, n_keep, slot_off, head_select, pool_k
 
 struct StepBuildArgs {
   const int32_t* state;
@@ -38,7 +40,7 @@ struct StepBuildArgs {
   int32_t* dense_ids;   // [max(1, n)]
   int32_t* cached_ids;  // [max(1, n)]
   int32_t* slot_off;    // [n+1]
-  int32_t* jobs;        // [max(1, n)][6]
+  int32_t* jobs;        // [max(1, n)][kJobCols]
   int32_t* slots;
   int slots_cap;
   int64_t* positions;
@@ -89,10 +91,13 @@ __global__ __launch_bounds__(1024) void step_build_kernel(StepBuildArgs a) {
   const int i = threadIdx.x;
   const bool live = i < a.n;
   int mode = -1, rows = 0, start = 0, bs = 0, bl = 0, keep = 0, wlo = 0, wn = 0, sr = 0, first = 0, err = 0;
+  int hsel = 0, pool = 1;
   if (live) {
     const int32_t* s = a.state + (int64_t)i * kStateCols;
     const int P = s[0], N = s[1], sparse = s[2], blen_cfg = s[3], bidx = s[4], sib = s[5], cs = s[6];
     const int steps = s[8], cur = s[9];
+    hsel = s[10];
+    pool = s[11];
     if (!sparse) {
       mode = 0;
       rows = N;
@@ -167,13 +172,15 @@ __global__ __launch_bounds__(1024) void step_build_kernel(StepBuildArgs a) {
       a.slot_off[c_at] = sbase;
     }
     if (mode == 1) {
-      int32_t* j = a.jobs + 6 * (int64_t)j_at;
+      int32_t* j = a.jobs + kJobCols * (int64_t)j_at;
       j[0] = cu0;
       j[1] = rows;
       j[2] = bs;
       j[3] = bl;
       j[4] = keep;
       j[5] = sbase;
+      j[6] = hsel;
+      j[7] = pool;
     }
     int32_t* p = a.smp_params + 5 * (int64_t)i;
     p[0] = (int32_t)((int64_t)i * a.tok_stride + wlo);
@@ -188,7 +195,7 @@ __global__ __launch_bounds__(1024) void step_build_kernel(StepBuildArgs a) {
     if (n_dense == 0) a.dense_ids[0] = 0;
     if (n_cached == 0) a.cached_ids[0] = 0;
     if (n_job == 0)
-      for (int c = 0; c < 6; ++c) a.jobs[c] = 0;
+      for (int c = 0; c < kJobCols; ++c) a.jobs[c] = 0;
     a.counts[0] = tot_rows;
     a.counts[1] = n_dense;
     a.counts[2] = n_cached;

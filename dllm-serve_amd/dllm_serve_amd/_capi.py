@@ -51,11 +51,11 @@ SIGNATURES = {
         [_P, _P, _P, _P, _P, _P, _I, _I, _I, _P, _P, _I64, _P, _P, _I, _I, _I,
          _I64, _I64, _I64, _I64, _F, _P],
     ),
-    "dllm_select_kv_workspace_size": (_SZ, [_I, _I, _I, _I, _I, _I]),
+    "dllm_select_kv_workspace_size": (_SZ, [_I, _I, _I, _I, _I]),
     "dllm_select_kv_store": (
         _I,
-        [_P, _P, _P, _I64, _I64, _I64, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _F,
-         _P, _P, _I64, _P, _P, _P, _SZ, _P],
+        [_P, _P, _P, _I64, _I64, _I64, _I64, _P, _I, _I, _I, _I, _I, _I, _F,
+         _P, _P, _I64, _P, _I64, _P, _P, _SZ, _P],
     ),
     "dllm_rope_neox": (_I, [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _P, _I64, _I, _I, _I, _I, _P]),
     "dllm_softmax_max_workspace_size": (_SZ, [_I, _I]),
@@ -198,23 +198,26 @@ def attn_block_cached_fwd_noalloc(q, k, v, o, cu, seg_ids, n_seg, max_q, max_key
     _check(rc, "dllm_attn_block_cached_fwd_noalloc")
 
 
-def select_workspace_size(n_job, max_kc, Hq, Hkv, D, head_select) -> int:
-    return int(load().dllm_select_kv_workspace_size(n_job, max_kc, Hq, Hkv, D, int(bool(head_select))))
+JOB_COLS = 8  # row0, n_tok, blk_start, blk_len, n_keep, slot_off, head_select, pool_k
 
 
-def select_kv_store(q, k, v, jobs, n_job, max_kc, max_keep, max_blk, head_select, pool_k,
-                    sqrt_d, k_cache, v_cache, slots, idx_out, workspace):
-    """K5/K6: selection + fused cache scatter (see include/dllm_attn.h)."""
+def select_workspace_size(n_job, max_kc, Hq, Hkv, D) -> int:
+    return int(load().dllm_select_kv_workspace_size(n_job, max_kc, Hq, Hkv, D))
+
+
+def select_kv_store(q, k, v, jobs, n_job, max_kc, max_keep, sqrt_d, k_cache, v_cache, slots, idx_out, workspace):
+    """K5/K6: selection + fused cache scatter; jobs int32 [n_job, 8] carry each
+    sequence's head_select and pool_kernel (see include/dllm_attn.h)."""
     _require_gpu(q, k, v, jobs, k_cache, v_cache, slots)
     lib = load()
     Hq, Hkv, D = q.shape[1], k.shape[1], q.shape[2]
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
     rc = lib.dllm_select_kv_store(
-        q.data_ptr(), k.data_ptr(), v.data_ptr(), q.stride(0), k.stride(0), v.stride(0),
-        jobs.data_ptr(), n_job, max_kc, max_keep, max_blk, Hq, Hkv, D,
-        int(bool(head_select)), int(pool_k), float(sqrt_d),
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), min(q.shape[0], k.shape[0], v.shape[0]),
+        q.stride(0), k.stride(0), v.stride(0),
+        jobs.data_ptr(), n_job, max_kc, max_keep, Hq, Hkv, D, float(sqrt_d),
         k_cache.data_ptr(), v_cache.data_ptr(), k_cache.numel() // (Hkv * D),
-        slots.data_ptr(), _ptr(idx_out), _ptr(workspace), ws_bytes, _stream(q.device))
+        slots.data_ptr(), slots.numel(), _ptr(idx_out), _ptr(workspace), ws_bytes, _stream(q.device))
     _check(rc, "dllm_select_kv_store")
 
 

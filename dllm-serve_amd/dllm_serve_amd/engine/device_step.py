@@ -33,7 +33,7 @@ from ..layers.attention import StepLayout, StepPlan
 from ..utils.context import get_context, reset_context, set_context
 from .sampler import MAX_WINDOW, step_windows
 
-STATE_COLS = 10
+STATE_COLS = 12
 
 
 def state_row(seq) -> list[int]:
@@ -41,9 +41,10 @@ def state_row(seq) -> list[int]:
     st = seq.sparse_state
     steps = seq.sampling_params.steps if getattr(seq, "sampling_params", None) is not None else seq.steps
     if st is None:
-        return [seq.num_prompt_tokens, seq.num_tokens, 0, 1, 0, 0, 0, 0, steps, seq.current_step]
+        return [seq.num_prompt_tokens, seq.num_tokens, 0, 1, 0, 0, 0, 0, steps, seq.current_step, 0, 1]
     return [seq.num_prompt_tokens, seq.num_tokens, 1, st.block_len, st.current_block_idx, st.step_in_block,
-            st.cache_state, st.config.delay_step, steps, seq.current_step]
+            st.cache_state, st.config.delay_step, steps, seq.current_step, int(bool(st.config.head_select)),
+            int(st.config.pool_kernel)]
 
 
 @dataclass
@@ -89,7 +90,8 @@ class DeviceStepState:
         rows_cap = sum(s.num_tokens for s in seqs)
         slots_cap = max(1, sum(s.num_tokens for s in seqs if s.sparse_state is not None))
         m = max(1, n)
-        i32 = torch.zeros((n + 1) + m + m + (n + 1) + 6 * m + 5 * n + 8, dtype=torch.int32, device=self.device)
+        jc = _capi.JOB_COLS
+        i32 = torch.zeros((n + 1) + m + m + (n + 1) + jc * m + 5 * n + 8, dtype=torch.int32, device=self.device)
         o = 0
 
         def take(k):
@@ -99,7 +101,7 @@ class DeviceStepState:
             return v
 
         self.cu, self.dense_ids, self.cached_ids = take(n + 1), take(m), take(m)
-        self.slot_off, self.jobs = take(n + 1), take(6 * m)
+        self.slot_off, self.jobs = take(n + 1), take(jc * m)
         self.smp_params, self.counts = take(5 * n).view(n, 5), take(8)
         self.slots = torch.zeros(slots_cap, dtype=torch.int32, device=self.device)
         self.positions = torch.zeros(rows_cap, dtype=torch.int64, device=self.device)
@@ -124,7 +126,7 @@ class DeviceStepState:
                          self.token_index, self.smp_params, self.smp_rows, self.counts)
         plan = StepPlan.from_device(lay, self.device, self.cu, self.dense_ids[:max(1, lay.n_dense)],
                                     self.cached_ids[:max(1, lay.n_cached)], self.slot_off[:lay.n_cached + 1],
-                                    self.jobs[:6 * max(1, lay.n_job)], self.slots)
+                                    self.jobs[:_capi.JOB_COLS * max(1, lay.n_job)], self.slots)
         return StepTables(lay, plan, self.positions[:lay.total_rows], self.token_index[:lay.total_rows],
                           self.smp_params, self.smp_rows[:n_win], max((w[2] for w in wins), default=0),
                           self.counts)

@@ -88,8 +88,10 @@ class StepLayout:
     def __init__(self, seqs):
         if not seqs:
             raise ValueError("diffusion context has no sequences")
-        rows, modes, spans, keeps = [], [], [], []
+        rows, modes, spans, keeps, cfgs = [], [], [], [], []
         for seq in seqs:
+            cfg = seq.sparse_state.config if seq.sparse_state is not None else None
+            cfgs.append((bool(cfg.head_select), int(cfg.pool_kernel)) if cfg is not None else (False, 1))
             st = seq.sparse_state
             N = seq.num_tokens
             if st is None or st.is_full_attention:
@@ -123,6 +125,7 @@ class StepLayout:
                 spans.append((0, 0))
                 keeps.append(0)
         self.modes, self.rows, self.spans, self.keeps = modes, rows, spans, keeps
+        self.cfgs = cfgs  # (head_select, pool_kernel) per sequence; selection jobs carry their own
         self.n_seq = len(seqs)
         self.total_rows = int(sum(rows))
         self.cu = np.zeros(self.n_seq + 1, dtype=np.int64)
@@ -144,20 +147,11 @@ class StepLayout:
         self.max_q_cached = max((rows[i] for i in self.cached), default=0)
         self.max_keys_cached = max((rows[i] + keeps[i] for i in self.cached), default=0)
         self.total_slots = sum(keeps[i] for i in self.cached + self.jobs_idx)
-        self.head_select = None
-        self.pool_k = None
-        for i in self.jobs_idx:
-            cfg = seqs[i].sparse_state.config
-            hs, pk = bool(cfg.head_select), int(cfg.pool_kernel)
-            if self.head_select is None:
-                self.head_select, self.pool_k = hs, pk
-            elif (hs, pk) != (self.head_select, self.pool_k):
-                raise NotImplementedError("sequences with different head_select / pool_kernel in one step")
 
     def signature(self) -> tuple:
         """Everything a captured step's launches depend on."""
         return (tuple(self.modes), tuple(self.rows), tuple(self.keeps), tuple(s[1] for s in self.spans),
-                self.head_select, self.pool_k)
+                tuple(self.cfgs[i] for i in self.jobs_idx))
 
 
 class StepPlan:
@@ -168,7 +162,7 @@ class StepPlan:
     ``StepPlan.from_device`` wraps tables the device-side builder wrote."""
 
     _SCALARS = ("n_seq", "total_rows", "any_skipped", "n_dense", "max_q_dense", "n_job", "max_kc", "max_keep",
-                "max_blk", "n_cached", "max_q_cached", "max_keys_cached", "head_select", "pool_k")
+                "max_blk", "n_cached", "max_q_cached", "max_keys_cached")
 
     def __init__(self, context, device: torch.device, num_kv_heads: int = 0, head_dim: int = 0, num_heads: int = 0,
                  layout: StepLayout | None = None):
@@ -196,11 +190,12 @@ class StepPlan:
             slot_parts.append(_slot_tensor(sm, device))
         self.slots = torch.cat(slot_parts) if slot_parts else torch.zeros(1, dtype=torch.int32, device=device)
 
-        # selection jobs: row0, n_tok, blk_start, blk_len, n_keep, slot_off
-        jobs = np.zeros((max(1, self.n_job), 6), dtype=np.int64)
+        # selection jobs: row0, n_tok, blk_start, blk_len, n_keep, slot_off, head_select, pool_k
+        jobs = np.zeros((max(1, self.n_job), _capi.JOB_COLS), dtype=np.int64)
         for r, i in enumerate(jobs_idx):
             bs, bl = spans[i]
-            jobs[r] = (cu[i], rows[i], bs, bl, keeps[i], slot_base[i])
+            hs, pk = lay.cfgs[i]
+            jobs[r] = (cu[i], rows[i], bs, bl, keeps[i], slot_base[i], int(hs), pk)
 
         # cached (state 2) segments: slot offsets indexed by position in `cached`
         slot_off = np.zeros(self.n_cached + 1, dtype=np.int64)
@@ -284,6 +279,15 @@ class Attention(nn.Module):
             context._dllm_plan = plan
         return plan
 
+    def _check_cache(self, device) -> None:
+        # the kernels address the bound cache as flat bf16 rows of Hkv * head_dim
+        # elements on q's device (the checks store_kvcache makes, attention.py:42-47)
+        for t, n in ((self.k_cache, "k_cache"), (self.v_cache, "v_cache")):
+            if (t.dtype != torch.bfloat16 or not t.is_contiguous() or t.device != device or t.dim() < 2
+                    or tuple(t.shape[-2:]) != (self.num_kv_heads, self.head_dim)):
+                raise ValueError(f"{n} must be a contiguous bf16 tensor [..., {self.num_kv_heads}, {self.head_dim}] "
+                                 f"on {device}; got {t.dtype} {tuple(t.shape)} on {t.device}")
+
     def _mixed_sparse_dense_attention(self, q, k, v, context):
         for t, n in ((q, "q"), (k, "k"), (v, "v")):
             _check_rows(t, n)
@@ -305,20 +309,19 @@ class Attention(nn.Module):
         if plan.n_job:
             if not (self.k_cache.numel() and self.v_cache.numel()):
                 raise RuntimeError("cache state 1 needs k_cache/v_cache bound to this layer")
-            ws = plan.workspace("select", _capi.select_workspace_size(
-                plan.n_job, plan.max_kc, Hq, Hkv, D, plan.head_select))
-            n_sel = Hkv if plan.head_select else 1
+            self._check_cache(q.device)
+            ws = plan.workspace("select", _capi.select_workspace_size(plan.n_job, plan.max_kc, Hq, Hkv, D))
             idx = None
             if self.keep_indices:
-                idx = torch.full((plan.n_job, n_sel, plan.max_keep), -1, dtype=torch.int64, device=q.device)
-            _capi.select_kv_store(q, k, v, plan.jobs, plan.n_job, plan.max_kc, plan.max_keep, plan.max_blk,
-                                  plan.head_select, plan.pool_k, np.float32(D ** 0.5),
+                idx = torch.full((plan.n_job, Hkv, plan.max_keep), -1, dtype=torch.int64, device=q.device)
+            _capi.select_kv_store(q, k, v, plan.jobs, plan.n_job, plan.max_kc, plan.max_keep, np.float32(D ** 0.5),
                                   self.k_cache, self.v_cache, plan.slots, idx, ws)
             self.last_select_indices = idx
 
         if plan.n_cached:
             if not (self.k_cache.numel() and self.v_cache.numel()):
                 raise RuntimeError("cache state 2 needs k_cache/v_cache bound to this layer")
+            self._check_cache(q.device)
             ws = plan.workspace("cached", _capi.block_cached_workspace_size(
                 plan.n_cached, plan.max_q_cached, plan.max_keys_cached, Hq, Hkv, D))
             _capi.attn_block_cached_fwd(q, k, v, o, plan.cu, plan.cached_ids, plan.n_cached,

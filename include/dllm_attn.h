@@ -154,37 +154,44 @@ int dllm_attn_block_cached_fwd_noalloc(const dllm_bf16* q, const dllm_bf16* k, c
  * "compute cache").  Replaces _select_important_head_kv (head_select != 0,
  * dllmserve/layers/attention.py:344-413), _select_important_kv (head_select
  * == 0, attention.py:308-342) and the store_kvcache call that follows them
- * (attention.py:189-233).
+ * (attention.py:189-233).  Each job carries its own head_select and
+ * pool_kernel (the reference reads both per sequence, attention.py:211,329,
+ * 387), so one call serves a step mixing SparseConfigs.
  *
- * jobs is an int32 array [n_job][6]: {row0, n_tok, blk_start, blk_len,
- * n_keep, slot_off}.  For job j the sequence occupies q/k/v rows
- * [row0, row0+n_tok); the current block is rows [blk_start, blk_start+blk_len)
- * of the sequence; the candidates are the other Kc = n_tok - blk_len rows in
- * order (prefix, then suffix).  Per selection head (each KV head when
- * head_select != 0, one shared head otherwise) the n_keep candidates with the
- * highest pooled score are written, best first, to cache slots
- * slots[slot_off + r], r in [0, n_keep).  Scoring rule (deterministic;
- * bit-exact against the oracle):
+ * jobs is an int32 array [n_job][8]: {row0, n_tok, blk_start, blk_len, n_keep,
+ * slot_off, head_select, pool_k}.  For job j the sequence occupies q/k/v rows
+ * [row0, row0+n_tok) (within [0, n_rows)); the current block is rows
+ * [blk_start, blk_start+blk_len) of the sequence; the candidates are the
+ * other Kc = n_tok - blk_len rows in order (prefix, then suffix).  Per
+ * selection head (each KV head when head_select != 0, one shared head
+ * otherwise) the n_keep candidates with the highest pooled score are written,
+ * best first, to cache slots slots[slot_off + r], r in [0, n_keep)
+ * (slot_off + n_keep <= n_slots).  Scoring rule (deterministic; bit-exact
+ * against the oracle), with g = Hq / Hkv and dot(h, j) = f64 sum over d
+ * ascending of qbar[h, d] * k[cand j, h / g, d]:
  *   qbar[h, d]  = bf16(f32(f64 sum_t q[blk_start+t, h, d], t ascending) / blk_len))
- *   raw[g, j]   = bf16(f32(f64 sum_d qbar[h_g, d] * k[cand j, kv, d], d ascending))
- *                 (head_select == 0: one sum over h ascending then d ascending,
- *                  with kv = h / (Hq/Hkv))
- *   score[j]    = bf16(f32(max_g raw[g, j]) / f32(sqrt(D)))   (IEEE division)
+ *   raw[kv, j]  = max over the g query heads h of KV head kv of bf16(f32(dot(h, j)))
+ *                 (head_select == 0: one raw[j] = bf16(f32(sum over kv ascending of
+ *                  (sum over h of kv's group ascending of dot(h, j)))), f64 sums)
+ *   score[j]    = bf16(f32(raw[j]) / f32(sqrt(D)))   (IEEE division)
  *   pooled[j]   = max of score over [j - pool_k/2, j - pool_k/2 + pool_k - 1]
  *                 clipped to the candidates (no pooling when pool_k <= 1)
  *   order: pooled descending, then candidate index ascending.
- * idx_out (nullable) receives the selected candidate indices as int64
- * [n_job][n_sel_heads][max_keep] (n_sel_heads = Hkv or 1; entries r >= n_keep
- * of a job are not written).  Kc must be <= 8192.  workspace must hold
- * dllm_select_kv_workspace_size(...) bytes.
+ * There is no limit on Kc.  idx_out (nullable) receives the selected
+ * candidate indices as int64 [n_job][Hkv][max_keep] (a head_select == 0 job
+ * writes row 0 of its entry only; entries r >= n_keep are not written).
+ * Jobs are clamped to the launch sizes: Kc to max_kc, n_keep to
+ * min(max_keep, Kc); a job whose rows, block or slots fall outside the given
+ * sizes selects and writes nothing.  workspace must hold
+ * dllm_select_kv_workspace_size(...) bytes, 16-byte aligned.
  */
-size_t dllm_select_kv_workspace_size(int n_job, int max_kc, int Hq, int Hkv, int D, int head_select);
-int dllm_select_kv_store(const dllm_bf16* q, const dllm_bf16* k, const dllm_bf16* v,
+size_t dllm_select_kv_workspace_size(int n_job, int max_kc, int Hq, int Hkv, int D);
+int dllm_select_kv_store(const dllm_bf16* q, const dllm_bf16* k, const dllm_bf16* v, int64_t n_rows,
                          int64_t q_stride_tok, int64_t k_stride_tok, int64_t v_stride_tok,
-                         const int32_t* jobs, int n_job, int max_kc, int max_keep, int max_blk,
-                         int Hq, int Hkv, int D, int head_select, int pool_k, float sqrt_d,
+                         const int32_t* jobs, int n_job, int max_kc, int max_keep,
+                         int Hq, int Hkv, int D, float sqrt_d,
                          dllm_bf16* k_cache, dllm_bf16* v_cache, int64_t cache_slots,
-                         const int32_t* slots, int64_t* idx_out,
+                         const int32_t* slots, int64_t n_slots, int64_t* idx_out,
                          void* workspace, size_t workspace_bytes, void* stream);
 
 /*
@@ -284,9 +291,10 @@ int dllm_lowconf_unmask(int64_t* tokens, int64_t n_tokens, const int32_t* seq_pa
  * attention.py:168-265, sequence.py:99-152) and the sampler's windows
  * (model_runner.py:791-818,911-920).
  *
- * seq_state is int32 [n_seq][10] per sequence: {P (prompt tokens), N (all
+ * seq_state is int32 [n_seq][12] per sequence: {P (prompt tokens), N (all
  * tokens), sparse (0: no SparseConfig), block_len, current_block_idx,
- * step_in_block, cache_state, delay_step, steps, current_step}; ratio is the
+ * step_in_block, cache_state, delay_step, steps, current_step, head_select,
+ * pool_kernel}; ratio is the
  * f64 retention ratio per sequence.  Sequence b's cache pages are
  * pages[page_off[b] .. page_off[b+1]).  Outputs, for the step the state
  * describes (n = n_seq):
@@ -296,8 +304,9 @@ int dllm_lowconf_unmask(int64_t* tokens, int64_t n_tokens, const int32_t* seq_pa
  *                        first (ties by index)
  *   cached_ids [max(1,n)] sequences in state 2, in order
  *   slot_off [n+1]      their slot ranges in `slots`
- *   jobs [max(1,n)][6]  state-1 selection jobs {row0, n_tok, blk_start,
- *                       blk_len, n_keep, slot_off} (as dllm_select_kv_store)
+ *   jobs [max(1,n)][8]  state-1 selection jobs {row0, n_tok, blk_start,
+ *                       blk_len, n_keep, slot_off, head_select, pool_k} (as
+ *                       dllm_select_kv_store)
  *   slots [slots_cap]   n_keep slots per state-2 sequence, then per state-1
  *                       sequence: page[r / 256] * 256 + r % 256 (-1 past its pages)
  *   positions, token_index [rows_cap] (int64) position of each fed row and

@@ -8,8 +8,11 @@ group, max_pool1d, topk); its accumulation order and topk tie order are
 those of the device libraries and are not specified.  The build fixes them:
 
   qbar[h,d]   = bf16( f32( (sum_t q[t,h,d]) / Lb ) ), sum in f64, t ascending
-  raw[h,j]    = bf16( f32( sum_d qbar[h,d] * k[j, h//g, d] ) ), f64, d ascending
-                (head_select=False: one sum over h ascending, then d ascending)
+  dot[h,j]    = sum_d qbar[h,d] * k[j, h//g, d]   in f64, d ascending
+  raw[h,j]    = bf16( f32( dot[h,j] ) )                       (head_select=True)
+  raw[j]      = bf16( f32( sum_kv ( sum_{h in group kv} dot[h,j] ) ) )
+                f64, groups kv ascending, heads ascending inside a group
+                (head_select=False)
   score[kv,j] = bf16( f32(max_{h in group kv} raw[h,j]) / f32(sqrt(D)) )
   pooled[j]   = max score over [j - p//2, j - p//2 + p - 1] within [0, Kc)
                 (p = pool_kernel; none when p <= 1)
@@ -36,29 +39,41 @@ def qbar(q_blk: np.ndarray) -> np.ndarray:
     return bf16_bits_to_f32(f64_to_bf16_bits(acc / np.float64(Lb)))
 
 
-def raw_scores(qb: np.ndarray, k_cand: np.ndarray, head_select: bool) -> np.ndarray:
-    """qb [Hq, D], k_cand [Kc, Hkv, D] -> head_select: [Hq, Kc]; else [Kc]
-    (bf16 values as f32) before the division by sqrt(D)."""
+def dots(qb: np.ndarray, k_cand: np.ndarray) -> np.ndarray:
+    """dot[h, j] = sum_d qb[h, d] * k_cand[j, h // g, d] in f64, d ascending
+    ([Hq, Kc]).  Products of two bf16 values are exact in f64, so only the
+    order of the additions is a choice."""
     Hq, D = qb.shape
     Kc, Hkv, _ = k_cand.shape
     g = Hq // Hkv
     q64 = qb.astype(np.float64)
     k64 = k_cand.astype(np.float64)
-    if head_select:
-        out = np.empty((Hq, Kc), dtype=np.float32)
-        for h in range(Hq):
-            acc = np.zeros(Kc, dtype=np.float64)
-            kh = k64[:, h // g, :]
-            for d in range(D):
-                acc = acc + q64[h, d] * kh[:, d]
-            out[h] = bf16_bits_to_f32(f64_to_bf16_bits(acc))
-        return out
-    acc = np.zeros(Kc, dtype=np.float64)
+    out = np.empty((Hq, Kc), dtype=np.float64)
     for h in range(Hq):
+        acc = np.zeros(Kc, dtype=np.float64)
         kh = k64[:, h // g, :]
         for d in range(D):
             acc = acc + q64[h, d] * kh[:, d]
-    return bf16_bits_to_f32(f64_to_bf16_bits(acc))
+        out[h] = acc
+    return out
+
+
+def raw_scores(qb: np.ndarray, k_cand: np.ndarray, head_select: bool) -> np.ndarray:
+    """qb [Hq, D], k_cand [Kc, Hkv, D] -> head_select: [Hq, Kc]; else [Kc]
+    (bf16 values as f32) before the division by sqrt(D)."""
+    Hq = qb.shape[0]
+    Kc, Hkv, _ = k_cand.shape
+    g = Hq // Hkv
+    dt = dots(qb, k_cand)
+    if head_select:
+        return bf16_bits_to_f32(f64_to_bf16_bits(dt)).reshape(Hq, Kc)
+    total = np.zeros(Kc, dtype=np.float64)
+    for kv in range(Hkv):
+        part = np.zeros(Kc, dtype=np.float64)
+        for gi in range(g):
+            part = part + dt[kv * g + gi]
+        total = total + part
+    return bf16_bits_to_f32(f64_to_bf16_bits(total))
 
 
 def pool(s: np.ndarray, pool_k: int) -> np.ndarray:

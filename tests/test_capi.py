@@ -38,8 +38,12 @@ def test_workspace_size_functions():
     assert _capi.block_cached_workspace_size(1024, 32, 4000, 32, 32, 128) == 0
     ws = _capi.block_cached_workspace_size(2, 32, 4128, 32, 32, 128)
     assert ws > 0 and ws % 4 == 0
-    assert _capi.select_workspace_size(4, 1216, 32, 32, 128, True) >= 4 * 32 * 128 * 2 + 4 * 32 * 1216 * 2
-    assert _capi.select_workspace_size(0, 10, 32, 32, 128, True) == 0
+    # qbar, raw scores, token-selection partial sums, order keys, selections
+    assert _capi.select_workspace_size(4, 1216, 32, 32, 128) >= 4 * 32 * 128 * 2 + 4 * 32 * 1216 * (2 + 8 + 2 + 4)
+    assert _capi.select_workspace_size(0, 10, 32, 32, 128) == 0
+    # beyond the in-LDS sort the radix-sort ping-pong buffers are added
+    small = _capi.select_workspace_size(1, 8192, 32, 32, 128)
+    assert _capi.select_workspace_size(1, 8193, 32, 32, 128) >= small + 2 * 32 * 8193 * (2 + 4)
 
 
 def _err(rc):
@@ -67,9 +71,17 @@ def test_argument_validation_without_gpu():
                                                   4096, fake, fake, 32, 32, 128, 4096, 4096, 4096, 4096, 0.1,
                                                   None, 0, None))
     assert rc == _capi.DLLM_ERR_WORKSPACE
-    rc, msg = _err(lib.dllm_select_kv_store(fake, fake, fake, 4096, 4096, 4096, fake, 1, 9000, 100, 64, 32, 32,
-                                            128, 1, 3, 11.3, fake, fake, 4096, fake, None, fake, 1 << 20, None))
-    assert rc == _capi.DLLM_ERR_UNSUPPORTED and "8192" in msg
+    # selection: no candidate cap any more; the workspace and the group size are checked
+    need = _capi.select_workspace_size(1, 9000, 32, 32, 128)
+    rc, msg = _err(lib.dllm_select_kv_store(fake, fake, fake, 9064, 4096, 4096, 4096, fake, 1, 9000, 100, 32, 32,
+                                            128, 11.3, fake, fake, 4096, fake, 100, None, fake, need - 1, None))
+    assert rc == _capi.DLLM_ERR_WORKSPACE
+    rc, msg = _err(lib.dllm_select_kv_store(fake, fake, fake, 9064, 65 * 128, 128, 128, fake, 1, 9000, 100, 65, 1,
+                                            128, 11.3, fake, fake, 4096, fake, 100, None, fake, 1 << 30, None))
+    assert rc == _capi.DLLM_ERR_UNSUPPORTED and "query heads per KV head" in msg
+    rc, msg = _err(lib.dllm_select_kv_store(fake, fake, fake, 9064, 4096, 4096, 4096, fake, 1, 90, 100, 32, 32,
+                                            128, 11.3, fake, fake, 4096, fake, 100, None, fake, 1 << 30, None))
+    assert rc == _capi.DLLM_ERR_INVALID_ARG and "max_keep" in msg
     rc, msg = _err(lib.dllm_store_kvcache(None, 4096, None, 4096, None, None, 10, None, 3, 4096, None))
     assert rc == _capi.DLLM_ERR_INVALID_ARG
     assert lib.dllm_store_kvcache(None, 4096, None, 4096, None, None, 10, None, 0, 4096, None) == 0

@@ -42,17 +42,17 @@ def test_select_fixtures(dev):
         k = torch.zeros(n_tok, Hkv, 128, dtype=torch.bfloat16)
         k[Lb:] = kb
         v = k.clone()
-        jobs = torch.tensor([[0, n_tok, 0, Lb, n_keep, 0]], dtype=torch.int32, device=dev)
+        jobs = torch.tensor([[0, n_tok, 0, Lb, n_keep, 0, hs, pk]], dtype=torch.int32, device=dev)
         cache = torch.zeros(2, 256, Hkv, 128, dtype=torch.bfloat16, device=dev)
         slots = torch.arange(n_keep, dtype=torch.int32, device=dev)
-        n_sel = Hkv if hs else 1
-        idx = torch.full((1, n_sel, n_keep), -1, dtype=torch.int64, device=dev)
-        ws = torch.empty(_capi.select_workspace_size(1, Kc, Hq, Hkv, 128, hs), dtype=torch.uint8, device=dev)
-        _capi.select_kv_store(q.to(dev), k.to(dev), v.to(dev), jobs, 1, Kc, n_keep, Lb, hs, pk,
+        idx = torch.full((1, Hkv, n_keep), -1, dtype=torch.int64, device=dev)
+        ws = torch.empty(_capi.select_workspace_size(1, Kc, Hq, Hkv, 128), dtype=torch.uint8, device=dev)
+        _capi.select_kv_store(q.to(dev), k.to(dev), v.to(dev), jobs, 1, Kc, n_keep,
                               np.float32(128 ** 0.5), cache[0], cache[1], slots, idx, ws)
         torch.cuda.synchronize()
+        got = idx.cpu().numpy()[0] if hs else idx.cpu().numpy()[0][:1]
         want = fx[f"{name}_idx"] if hs else fx[f"{name}_idx"][None, :]
-        assert np.array_equal(idx.cpu().numpy()[0], want), name
+        assert np.array_equal(got, want), name
 
 
 def test_rope_fixture(dev):

@@ -10,20 +10,85 @@ from helpers import bits, to_np
 from oracle import select as osel
 from oracle import kvcache as okv
 from dllm_serve_amd import _capi
-from dllm_serve_amd.sparse.state import keep_count
+from dllm_serve_amd.engine.sequence import PageAllocator, Sequence, slot_mapping_for
+from dllm_serve_amd.sparse.state import SparseConfig, keep_count
 
 pytestmark = pytest.mark.gpu
 
+D = 128
 
-def _job_case(n_tok, bs, bl, Hq, Hkv, seed, n_slots_pages):
-    D = 128
+
+def _run_jobs(dev, q, k, v, specs, kc_cache, vc_cache, slots, max_kc=None, max_keep=None, ws_extra=0):
+    """specs: per job (row0, n_tok, bs, bl, n_keep, slot_off, head_select, pool_k).
+    Returns idx [n_job, Hkv, max_keep] (int64, -1 where unwritten) and the workspace."""
+    Hq, Hkv = q.shape[1], k.shape[1]
+    n_job = len(specs)
+    max_kc = max_kc if max_kc is not None else max(s[1] - s[3] for s in specs)
+    max_keep = max_keep if max_keep is not None else max(s[4] for s in specs)
+    jobs = torch.tensor(specs, dtype=torch.int32, device=dev)
+    idx = torch.full((n_job, Hkv, max_keep), -1, dtype=torch.int64, device=dev)
+    need = _capi.select_workspace_size(n_job, max_kc, Hq, Hkv, D)
+    ws = torch.empty(need + ws_extra, dtype=torch.uint8, device=dev)
+    if ws_extra:
+        ws[need:] = 0xA5
+    _capi.select_kv_store(q, k, v, jobs, n_job, max_kc, max_keep, np.float32(D ** 0.5), kc_cache, vc_cache,
+                          slots, idx, ws)
+    torch.cuda.synchronize()
+    return idx.cpu().numpy(), ws, need
+
+
+def _expected(q, k, v, spec, ref_kc, ref_vc, slots_np):
+    """Oracle selection of one job; stores the selected rows into the reference
+    caches (bit patterns) in place; returns the indices ([Hkv, n] or [n])."""
+    row0, n_tok, bs, bl, n_keep, soff, hs, pk = spec
+    qn, kn = to_np(q[row0:row0 + n_tok]), to_np(k[row0:row0 + n_tok])
+    Hkv = k.shape[1]
+    cand = np.concatenate([np.arange(0, bs), np.arange(bs + bl, n_tok)])
+    idx = osel.select(qn[bs:bs + bl], kn[cand], n_keep, bool(hs), pk, np.float32(D ** 0.5))
+    kb = bits(k[row0:row0 + n_tok]).reshape(n_tok, Hkv, D)
+    vb = bits(v[row0:row0 + n_tok]).reshape(n_tok, Hkv, D)
+    if hs:
+        hk = np.arange(Hkv)[None, :]
+        ksel, vsel = kb[cand][idx.T, hk], vb[cand][idx.T, hk]
+    else:
+        ksel, vsel = kb[cand][idx], vb[cand][idx]
+    okv.store(ksel.reshape(n_keep, -1), vsel.reshape(n_keep, -1), ref_kc, ref_vc, slots_np[soff:soff + n_keep])
+    return idx
+
+
+def _check(got, idx_ref, spec, what):
+    n_keep, hs = spec[4], spec[6]
+    g = got[:, :n_keep] if hs else got[:1, :n_keep]
+    want = idx_ref if hs else idx_ref[None, :]
+    mism = int((g != want).sum())
+    assert mism == 0, f"{what}: {mism} of {want.size} selected indices differ"
+
+
+def _inputs(n_tok, Hq, Hkv, seed):
     g = torch.Generator().manual_seed(seed)
     q = torch.randn(n_tok, Hq, D, generator=g).to(torch.bfloat16)
     k = torch.randn(n_tok, Hkv, D, generator=g).to(torch.bfloat16)
     v = torch.randn(n_tok, Hkv, D, generator=g).to(torch.bfloat16)
-    kc = torch.randn(n_slots_pages * 256, Hkv, D, generator=g).to(torch.bfloat16)
-    vc = torch.randn(n_slots_pages * 256, Hkv, D, generator=g).to(torch.bfloat16)
-    return q, k, v, kc, vc
+    return q, k, v
+
+
+def _one_job(dev, n_tok, bs, bl, Hq, Hkv, ratio, head_select, pool_k, seed):
+    Kc = n_tok - bl
+    n_keep = keep_count(Kc, ratio)
+    pages = -(-n_keep // 256) + 2
+    q, k, v = _inputs(n_tok, Hq, Hkv, seed)
+    g = torch.Generator().manual_seed(seed + 99)
+    kc = torch.randn(pages * 256, Hkv, D, generator=g).to(torch.bfloat16)
+    vc = torch.randn(pages * 256, Hkv, D, generator=g).to(torch.bfloat16)
+    slots = torch.randperm(pages * 256, generator=g)[:n_keep].to(torch.int32)
+    spec = (0, n_tok, bs, bl, n_keep, 0, int(head_select), pool_k)
+    ref_kc, ref_vc = bits(kc).reshape(-1, Hkv * D).copy(), bits(vc).reshape(-1, Hkv * D).copy()
+    idx_ref = _expected(q, k, v, spec, ref_kc, ref_vc, slots.numpy())
+    kcd, vcd = kc.to(dev), vc.to(dev)
+    got, _, _ = _run_jobs(dev, q.to(dev), k.to(dev), v.to(dev), [spec], kcd, vcd, slots.to(dev))
+    _check(got[0], idx_ref, spec, f"n_tok={n_tok}")
+    assert np.array_equal(bits(kcd).reshape(-1, Hkv * D), ref_kc)
+    assert np.array_equal(bits(vcd).reshape(-1, Hkv * D), ref_vc)
 
 
 CASES = [
@@ -42,89 +107,138 @@ CASES = [
 def test_select_store_bit_exact(dev, n_tok, bs, bl, Hq, Hkv, ratio, head_select, pool_k):
     print(f"select n_tok={n_tok} bs={bs} bl={bl} Hq={Hq} Hkv={Hkv} r={ratio} hs={head_select} p={pool_k}",
           flush=True)
-    D = 128
-    Kc = n_tok - bl
-    n_keep = keep_count(Kc, ratio)
-    pages = -(-n_keep // 256) + 2
-    q, k, v, kc, vc = _job_case(n_tok, bs, bl, Hq, Hkv, seed=n_tok + bs, n_slots_pages=pages)
-    g = torch.Generator().manual_seed(99)
-    slots = torch.randperm(pages * 256, generator=g)[:n_keep].to(torch.int32)
-
-    # oracle
-    qn, kn, vn = to_np(q), to_np(k), to_np(v)
-    cand = np.concatenate([np.arange(0, bs), np.arange(bs + bl, n_tok)])
-    idx_ref = osel.select(qn[bs:bs + bl], kn[cand], n_keep, head_select, pool_k, np.float32(D ** 0.5))
-    kb, vb = bits(k).reshape(n_tok, Hkv, D), bits(v).reshape(n_tok, Hkv, D)
-    if head_select:
-        hk = np.arange(Hkv)[None, :]
-        ksel, vsel = kb[cand][idx_ref.T, hk], vb[cand][idx_ref.T, hk]
-    else:
-        ksel, vsel = kb[cand][idx_ref], vb[cand][idx_ref]
-    ref_kc, ref_vc = bits(kc).reshape(-1, Hkv * D).copy(), bits(vc).reshape(-1, Hkv * D).copy()
-    okv.store(ksel.reshape(n_keep, -1), vsel.reshape(n_keep, -1), ref_kc, ref_vc, slots.numpy())
-
-    # GPU
-    jobs = torch.tensor([[0, n_tok, bs, bl, n_keep, 0]], dtype=torch.int32, device=dev)
-    kcd, vcd = kc.to(dev), vc.to(dev)
-    n_sel = Hkv if head_select else 1
-    idx = torch.full((1, n_sel, n_keep), -1, dtype=torch.int64, device=dev)
-    ws = torch.empty(_capi.select_workspace_size(1, Kc, Hq, Hkv, D, head_select), dtype=torch.uint8, device=dev)
-    _capi.select_kv_store(q.to(dev), k.to(dev), v.to(dev), jobs, 1, Kc, n_keep, bl, head_select, pool_k,
-                          np.float32(D ** 0.5), kcd, vcd, slots.to(dev), idx, ws)
-    torch.cuda.synchronize()
-    got = idx.cpu().numpy()[0]
-    ref = idx_ref if head_select else idx_ref[None, :]
-    mism = int((got != ref).sum())
-    assert mism == 0, f"{mism} of {got.size} selected indices differ"
-    assert np.array_equal(bits(kcd).reshape(-1, Hkv * D), ref_kc)
-    assert np.array_equal(bits(vcd).reshape(-1, Hkv * D), ref_vc)
+    _one_job(dev, n_tok, bs, bl, Hq, Hkv, ratio, head_select, pool_k, seed=n_tok + bs)
 
 
-def test_select_two_jobs_batched(dev):
-    """Two sequences in one launch, slots concatenated, different n_keep."""
-    print("select two jobs", flush=True)
-    D, Hq, Hkv = 128, 16, 16
-    specs = [(300, 256, 32, 0.5), (520, 256, 64, 0.3)]  # n_tok, bs, bl, ratio
-    g = torch.Generator().manual_seed(1234)
-    qs, ks, vs, jobs, slot_list = [], [], [], [], []
-    row0, soff = 0, 0
-    total_keep = sum(keep_count(n - bl, r) for n, _, bl, r in specs)
-    pages = -(-total_keep // 256) + 1
-    perm = torch.randperm(pages * 256, generator=g)
-    for n, bs, bl, r in specs:
-        qs.append(torch.randn(n, Hq, D, generator=g).to(torch.bfloat16))
-        ks.append(torch.randn(n, Hkv, D, generator=g).to(torch.bfloat16))
-        vs.append(torch.randn(n, Hkv, D, generator=g).to(torch.bfloat16))
-        nk = keep_count(n - bl, r)
-        jobs.append([row0, n, bs, bl, nk, soff])
-        slot_list.append(perm[soff:soff + nk])
-        row0 += n
+@pytest.mark.parametrize("n_tok,bs,bl,Hq,Hkv,ratio,head_select,pool_k", [
+    (12352, 12288, 64, 8, 8, 0.5, True, 3),    # 12288 candidates, 6144 kept: compaction, then the LDS sort
+    (12352, 6000, 64, 8, 4, 0.5, False, 3),    # the same with GQA token selection
+    (20032, 20000, 32, 4, 4, 0.9, True, 3),    # 18000 kept: the two-pass radix sort in the workspace
+    (20032, 100, 32, 4, 2, 0.75, False, 1),    # 15000 kept, token selection, no pooling
+])
+def test_select_beyond_8192_candidates(dev, n_tok, bs, bl, Hq, Hkv, ratio, head_select, pool_k):
+    """No candidate cap: the reference's torch.topk has none (attention.py:341,402-404)."""
+    print(f"select long n_tok={n_tok} Hq={Hq} Hkv={Hkv} r={ratio} hs={head_select} p={pool_k}", flush=True)
+    _one_job(dev, n_tok, bs, bl, Hq, Hkv, ratio, head_select, pool_k, seed=n_tok + Hkv)
+
+
+def test_select_summation_order(dev):
+    """Scores whose f64 sums are inexact, so the order of the additions decides
+    the result: q rows of one token (qbar = q exactly) hold +-2^60 at
+    d = 0 / 2 and ordinary values elsewhere, K holds 1 at those positions.
+    Summed d ascending, the ordinary term at d = 1 vanishes in 2^60; token
+    selection also adds KV-head partials of +-2^60 in head order.  The kernel
+    must follow the stated order exactly (oracle.select.dots / raw_scores)."""
+    print("select summation order (cancelling 2^60 terms)", flush=True)
+    for hs, Hq, Hkv in ((True, 4, 4), (False, 4, 4), (False, 8, 2)):
+        n_tok, bl = 300, 1
+        q, k, v = _inputs(n_tok, Hq, Hkv, seed=31 + Hq)
+        big = 2.0 ** 60
+        q[0, :, 0] = big
+        q[0, :, 2] = -big
+        if not hs:
+            # heads 0 / 1 end at +2^60 / -2^60: added in head order they cancel
+            # before the other heads' sums arrive, which then survive whole
+            q[0, 0, 3] = big
+            q[0, 1, 3] = -big
+        k[:, :, 0] = 1.0
+        k[:, :, 2] = 1.0
+        k[:, :, 3] = 1.0
+        Kc = n_tok - bl
+        spec = (0, n_tok, 0, bl, keep_count(Kc, 0.5), 0, int(hs), 3)
+        cache = torch.zeros(2, 256, Hkv, D, dtype=torch.bfloat16)
+        slots = torch.arange(spec[4], dtype=torch.int32)
+        ref_kc, ref_vc = bits(cache[0]).reshape(-1, Hkv * D).copy(), bits(cache[1]).reshape(-1, Hkv * D).copy()
+        idx_ref = _expected(q, k, v, spec, ref_kc, ref_vc, slots.numpy())
+        cd = cache.to(dev)
+        got, _, _ = _run_jobs(dev, q.to(dev), k.to(dev), v.to(dev), [spec], cd[0], cd[1], slots.to(dev))
+        _check(got[0], idx_ref, spec, f"hs={hs} Hq={Hq} Hkv={Hkv}")
+        assert np.array_equal(bits(cd[0]).reshape(-1, Hkv * D), ref_kc)
+
+
+def test_select_c4_four_jobs(dev):
+    """C4: B=4 sequences of 1024 prompt + 256 generated tokens, block 0 of the
+    generation (rows 1024..1087), retention 0.5, head_select, pool 3; slots
+    from slot_mapping_for over a shuffled page table; one launch."""
+    print("select C4 4 jobs x 1280 tokens, 32 heads", flush=True)
+    Hq = Hkv = 32
+    cfg = SparseConfig(enabled=True, default_block_len=64, retention_ratio=0.5, pool_kernel=3, head_select=True)
+    seqs = [Sequence([1] * 1024, 256, 126336, cfg, device="cpu") for _ in range(4)]
+    n_pages = sum(s.num_blocks for s in seqs) + 3
+    perm = torch.randperm(n_pages, generator=torch.Generator().manual_seed(4)).tolist()
+    alloc = PageAllocator(perm)
+    for s in seqs:
+        alloc.allocate(s)
+    q, k, v = _inputs(4 * 1280, Hq, Hkv, seed=1280)
+    specs, slot_list = [], []
+    for b, s in enumerate(seqs):
+        n_keep = keep_count(1280 - 64, 0.5)
+        s.sparse_state.cache_state = 1   # the block's selection step (delay_step 1, step 1)
+        sl = slot_mapping_for(s)
+        assert len(sl) == n_keep == 608
+        specs.append((b * 1280, 1280, 1024, 64, n_keep, b * n_keep, 1, 3))
+        slot_list.extend(sl)
+    slots = torch.tensor(slot_list, dtype=torch.int32)
+    cache = torch.zeros(2, n_pages * 256, Hkv, D, dtype=torch.bfloat16)
+    ref_kc, ref_vc = bits(cache[0]).reshape(-1, Hkv * D).copy(), bits(cache[1]).reshape(-1, Hkv * D).copy()
+    refs = [_expected(q, k, v, sp, ref_kc, ref_vc, slots.numpy()) for sp in specs]
+    cd = cache.to(dev)
+    got, _, _ = _run_jobs(dev, q.to(dev), k.to(dev), v.to(dev), specs, cd[0], cd[1], slots.to(dev))
+    for j, (sp, ref) in enumerate(zip(specs, refs)):
+        _check(got[j], ref, sp, f"job {j}")
+    assert np.array_equal(bits(cd[0]).reshape(-1, Hkv * D), ref_kc)
+    assert np.array_equal(bits(cd[1]).reshape(-1, Hkv * D), ref_vc)
+
+
+def test_select_mixed_configs_one_launch(dev):
+    """Jobs of one launch with head_select True / False and pool 1 / 3 / 5 and
+    different ratios (each SparseConfig read per sequence, attention.py:211,
+    329,387)."""
+    print("select mixed configs", flush=True)
+    Hq, Hkv = 16, 4
+    lens = [(300, 200, 32, 0.5, 1, 1), (520, 256, 64, 0.3, 0, 3), (260, 0, 16, 0.75, 1, 5), (400, 384, 16, 1.0, 0, 5)]
+    n = sum(x[0] for x in lens)
+    q, k, v = _inputs(n, Hq, Hkv, seed=77)
+    specs, row0, soff = [], 0, 0
+    for n_tok, bs, bl, r, hs, pk in lens:
+        nk = keep_count(n_tok - bl, r)
+        specs.append((row0, n_tok, bs, bl, nk, soff, hs, pk))
+        row0 += n_tok
         soff += nk
-    q, k, v = torch.cat(qs), torch.cat(ks), torch.cat(vs)
-    slots = torch.cat(slot_list).to(torch.int32)
-    kc = torch.zeros(pages * 256, Hkv, D, dtype=torch.bfloat16)
-    vc = torch.zeros_like(kc)
-    ref_kc, ref_vc = bits(kc).reshape(-1, Hkv * D).copy(), bits(vc).reshape(-1, Hkv * D).copy()
-    kb, vb = bits(k).reshape(-1, Hkv, D), bits(v).reshape(-1, Hkv, D)
-    refs = []
-    for (n, bs, bl, r), jb, sl in zip(specs, jobs, slot_list):
-        r0 = jb[0]
-        cand = np.concatenate([np.arange(0, bs), np.arange(bs + bl, n)]) + r0
-        idx_ref = osel.select(to_np(q)[r0 + bs:r0 + bs + bl], to_np(k)[cand], jb[4], True, 3, np.float32(D ** 0.5))
-        refs.append(idx_ref)
-        hk = np.arange(Hkv)[None, :]
-        okv.store(kb[cand][idx_ref.T, hk].reshape(jb[4], -1), vb[cand][idx_ref.T, hk].reshape(jb[4], -1),
-                  ref_kc, ref_vc, sl.numpy())
-    max_kc = max(n - bl for n, _, bl, _ in specs)
-    max_keep = max(j[4] for j in jobs)
-    kcd, vcd = kc.to(dev), vc.to(dev)
-    idx = torch.full((2, Hkv, max_keep), -1, dtype=torch.int64, device=dev)
-    ws = torch.empty(_capi.select_workspace_size(2, max_kc, Hq, Hkv, D, True), dtype=torch.uint8, device=dev)
-    _capi.select_kv_store(q.to(dev), k.to(dev), v.to(dev), torch.tensor(jobs, dtype=torch.int32, device=dev), 2,
-                          max_kc, max_keep, 64, True, 3, np.float32(D ** 0.5), kcd, vcd, slots.to(dev), idx, ws)
-    torch.cuda.synchronize()
-    got = idx.cpu().numpy()
-    for j, ref in enumerate(refs):
-        assert np.array_equal(got[j][:, :ref.shape[1]], ref)
-    assert np.array_equal(bits(kcd).reshape(-1, Hkv * D), ref_kc)
-    assert np.array_equal(bits(vcd).reshape(-1, Hkv * D), ref_vc)
+    pages = -(-soff // 256) + 1
+    slots = torch.randperm(pages * 256, generator=torch.Generator().manual_seed(3))[:soff].to(torch.int32)
+    cache = torch.zeros(2, pages * 256, Hkv, D, dtype=torch.bfloat16)
+    ref_kc, ref_vc = bits(cache[0]).reshape(-1, Hkv * D).copy(), bits(cache[1]).reshape(-1, Hkv * D).copy()
+    refs = [_expected(q, k, v, sp, ref_kc, ref_vc, slots.numpy()) for sp in specs]
+    cd = cache.to(dev)
+    got, _, _ = _run_jobs(dev, q.to(dev), k.to(dev), v.to(dev), specs, cd[0], cd[1], slots.to(dev))
+    for j, (sp, ref) in enumerate(zip(specs, refs)):
+        _check(got[j], ref, sp, f"job {j}")
+    assert np.array_equal(bits(cd[0]).reshape(-1, Hkv * D), ref_kc)
+    assert np.array_equal(bits(cd[1]).reshape(-1, Hkv * D), ref_vc)
+
+
+def test_select_jobs_clamped_to_launch_sizes(dev):
+    """Jobs that disagree with the launch sizes (more candidates than max_kc,
+    more rows kept than max_keep, slots past the slot list, rows past the
+    tensors) write nothing outside the workspace, the slot list or the cache:
+    guard bytes after the workspace stay intact, and a job whose slots or rows
+    overflow writes no cache row."""
+    print("select clamped jobs with a guarded workspace", flush=True)
+    Hq = Hkv = 8
+    n = 900
+    q, k, v = _inputs(n, Hq, Hkv, seed=5)
+    cache = torch.zeros(2, 512, Hkv, D, dtype=torch.bfloat16, device=dev)
+    slots = torch.arange(100, dtype=torch.int32, device=dev)
+    specs = [(0, 400, 300, 32, 300, 0, 1, 3),       # Kc 368 > max_kc 200, n_keep 300 > max_keep 50
+             (400, 300, 0, 32, 40, 80, 0, 3),       # slots 80..119: past the 100-entry slot list
+             (700, 300, 0, 32, 10, 0, 1, 3)]        # rows 700..999: past the 900 rows
+    got, ws, need = _run_jobs(dev, q.to(dev), k.to(dev), v.to(dev), specs, cache[0], cache[1], slots,
+                              max_kc=200, max_keep=50, ws_extra=4096)
+    assert torch.all(ws[need:] == 0xA5), "a kernel wrote past its workspace"
+    written = (cache[0].view(512, -1) != 0).any(dim=1).cpu().numpy()
+    assert not written[50:].any(), "rows beyond the first job's clamped 50 slots were written"
+    assert (got[1] == -1).all() and (got[2] == -1).all(), "jobs outside the launch sizes must select nothing"
+    # the clamped job selects its 50 best among its first 200 candidates (rows 0..199)
+    ref = osel.select(to_np(q)[300:332], to_np(k)[:200], 50, True, 3, np.float32(D ** 0.5))
+    assert np.array_equal(got[0][:, :50], ref), "clamped job"

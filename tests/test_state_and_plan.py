@@ -6,7 +6,7 @@ import pytest
 import torch
 
 from dllm_serve_amd.engine.sequence import PageAllocator, Sequence, prepare_step, slot_mapping_for
-from dllm_serve_amd.layers.attention import Attention, StepPlan, store_kvcache
+from dllm_serve_amd.layers.attention import Attention, StepLayout, StepPlan, store_kvcache
 from dllm_serve_amd.sparse.state import PerRequestSparseState, SparseConfig, keep_count
 from dllm_serve_amd.utils.context import get_context, reset_context, set_context
 
@@ -117,9 +117,33 @@ def test_step_plan_tables():
     n_c = keep_count(214 - 32, 0.5)   # 91
     assert plan.slot_off.tolist() == [0, n_b]
     assert plan.slots.tolist() == list(range(5 * 256, 5 * 256 + n_b)) + list(range(2 * 256, 2 * 256 + n_c))
-    assert plan.n_job == 1 and plan.jobs.tolist() == [196, 214, 150, 32, n_c, n_b]
-    assert plan.max_kc == 182 and plan.max_keep == n_c and plan.head_select is True and plan.pool_k == 3
+    # row0, n_tok, blk_start, blk_len, n_keep, slot_off, head_select, pool_k
+    assert plan.n_job == 1 and plan.jobs.tolist() == [196, 214, 150, 32, n_c, n_b, 1, 3]
+    assert plan.max_kc == 182 and plan.max_keep == n_c
     assert plan.max_q_cached == 32 and plan.max_keys_cached == 32 + n_b
+    reset_context()
+
+
+def test_step_plan_mixes_sparse_configs():
+    """Sequences of one step with different head_select / pool_kernel: each
+    selection job carries its own (the reference reads both per sequence,
+    attention.py:211,329,387)."""
+    cfgs = [SparseConfig(enabled=True, default_block_len=32, retention_ratio=0.5, head_select=True, pool_kernel=1),
+            SparseConfig(enabled=True, default_block_len=16, retention_ratio=0.25, head_select=False, pool_kernel=5),
+            SparseConfig(enabled=True, default_block_len=32, retention_ratio=1.0, head_select=True, pool_kernel=3)]
+    seqs = [Sequence([i + 1] * (100 + 40 * i), 64, MASK, c, device="cpu") for i, c in enumerate(cfgs)]
+    seqs.append(Sequence([9] * 50, 32, MASK, None, device="cpu"))
+    alloc = PageAllocator(range(8))
+    for s_ in seqs[:3]:
+        alloc.allocate(s_)
+        s_.sparse_state.cache_state = 1
+    prepare_step(seqs, "cpu")
+    plan = StepPlan(get_context(), torch.device("cpu"), 32, 128, 32)
+    jobs = plan.jobs.view(-1, 8).tolist()
+    assert plan.n_job == 3 and [j[6:] for j in jobs] == [[1, 1], [0, 5], [1, 3]]
+    assert [j[4] for j in jobs] == [keep_count(164 - 32, 0.5), keep_count(204 - 16, 0.25), 244 - 32]
+    lay = StepLayout(seqs)
+    assert lay.signature()[-1] == ((True, 1), (False, 5), (True, 3))
     reset_context()
 
 

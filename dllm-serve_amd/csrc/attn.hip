@@ -672,7 +672,48 @@ __device__ __forceinline__ void cached_merge_store(const AttnArgs& a, uint8_t* l
   }
 }
 
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void attn_cached_kernel(AttnArgs a) {
+
+// One 32-key block of the four-wavefront K3b: K operands from LDS, keys set in
+// `bad` left out of the softmax by a small conditional block (a single
+// softmax code path keeps the accumulators in place).
+__device__ __forceinline__ void cached_tile(const uint8_t* Ks, const uint8_t* Vs, const DenseAddr& ad,
+                                            const bf16x8_t (&qf)[1][8], DenseState<1>& st, float c, uint64_t bad) {
+  const int hl = (threadIdx.x & 63) >> 5;
+  f32x16_t sacc[1];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) sacc[0][i] = 0.f;
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk)
+    sacc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+        as_bf16x8(*reinterpret_cast<const u32x4_t*>(Ks + (ad.kbase ^ (uint32_t)(32 * kk)))), qf[0][kk], sacc[0], 0, 0, 0);
+  if (bad) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int key = 8 * (i >> 2) + 4 * hl + (i & 3);
+      if ((bad >> key) & 1ull) sacc[0][i] = -INFINITY;
+    }
+  }
+  bf16x8_t pf[2];
+  dense_softmax<1, false>(sacc, st.oacc[0], st.m_run[0], st.l_run[0], st.thr[0], st.neg_m[0], pf, c, 32, 0, hl);
+  // all 16 V^T operands are read (one asm block) before the first product:
+  // the MFMAs read their source registers after issue, so no register they
+  // use may be rewritten by a later LDS read while they run
+  u32x2_t vr[16];
+  v_operands_untracked(Vs, ad, vr);
+#pragma unroll
+  for (int cch = 0; cch < 2; ++cch)
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      const u32x2_t lo = vr[(4 * cch + db) * 2], hi = vr[(4 * cch + db) * 2 + 1];
+      st.oacc[0][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(u32x4_t{lo[0], lo[1], hi[0], hi[1]}), pf[cch],
+                                                               st.oacc[0][db], 0, 0, 0);
+    }
+}
+
+// Two wavefronts per SIMD as the register budget: the whole state then stays
+// in VGPRs (with a budget of 512 the compiler moves the O^T accumulators
+// between AGPRs and VGPRs around every softmax rescale).
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_cached_kernel(AttnArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int L = xcd_remap(blockIdx.x, a.xcd_chunk);
   if (L >= a.logical_blocks) return;
@@ -719,23 +760,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   // freed while tile t+1 is still in flight -- two tiles in flight per wave.
   // Vector memory operations complete in issue order, so each wait is "at
   // most N newer operations outstanding": a tile is 16 DMA instructions, a
-  // slot fetch 8 loads.
-  // The slot loads are issued as inline asm so that the compiler's own wait
-  // insertion does not track them: it would otherwise wait for every
-  // outstanding load around the loop.  Each slot is read only after an
-  // explicit vm_wait that retires it and an empty asm that ties the value to
-  // that point (slots_ready).
-  auto fetch_slots = [&](int (&dst)[8], int k0) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int kidx = k0 + 32 * wave + 4 * j + rl;
-      const int32_t* src = have_slots ? sp + min(max(kidx, 0), n_c - 1) : sp;
-      asm volatile("global_load_dword %0, %1, off" : "=v"(dst[j]) : "v"(src) : "memory");
-    }
+  // slot fetch one.
+  // The slots arrive by DMA too (lane l: the slot of key 32 wave + l of the
+  // tile) into a ring of four per-wave entries behind the stages, and lanes
+  // read them from LDS after the wait that retires the fetch: no register is
+  // ever written by a load the compiler does not know about.
+  uint32_t* slot_ring = reinterpret_cast<uint32_t*>(lds + 2 * CK_STAGE);  // [4 tiles][4 waves][64]
+  auto fetch_slots = [&](int t) {
+    const int kidx = kbeg + t * CK_TILE + 32 * wave + lrow;
+    const int32_t* src = have_slots ? sp + min(max(kidx, 0), n_c - 1) : sp;
+    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(slot_ring + ((t & 3) * 4 + wave) * 64),
+                                     4, 0, 0);
   };
-  auto slots_ready = [&](int (&v)[8]) {
+  // this lane's slots of tile t (rows 4j + rl of the wave's 32); call after the wait
+  auto read_slots = [&](int t, int (&dst)[8]) {
+    const uint32_t* e = slot_ring + ((t & 3) * 4 + wave) * 64;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) asm volatile("" : "+v"(v[j]));
+    for (int j = 0; j < 8; ++j) dst[j] = (int)e[4 * j + rl];
   };
   // Rows past kend read the last valid row; a cached row with an invalid
   // slot reads block row 0 (never the cache, which may be absent).  Both are
@@ -788,11 +829,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   // wait tracking, so no wait on q remains inside the tile loop), then D(0)
   // and D(1) together: tile 1 does not wait a second round trip.  Slot
   // fetches past the key range read a clamped, valid index and go unused.
-  int s0[8], s1[8];
-  int slot_ahead[8];          // slots of the next tile to issue: S(2) here
-  fetch_slots(s0, kbeg);
-  fetch_slots(s1, kbeg + CK_TILE);
-  fetch_slots(slot_ahead, kbeg + 2 * CK_TILE);
+  fetch_slots(0);
+  fetch_slots(1);
+  fetch_slots(2);
   const int m = m_base + lrow;
   const bool m_ok = m < M;
   const int tok = m_ok ? m / g : 0;
@@ -809,9 +848,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   const int ntiles = (kend - kbeg + CK_TILE - 1) / CK_TILE;
   uint32_t bad_t0 = 0, bad_t1 = 0;  // invalid-row masks of tiles t and t+1
   vm_wait<0>();  // S(0..2) and q
-  slots_ready(s0);
-  slots_ready(s1);
-  slots_ready(slot_ahead);
+  int s0[8], s1[8];
+  read_slots(0, s0);
+  read_slots(1, s1);
   if (ntiles > 0) {
     bad_t0 = invalid_rows(kbeg, s0);
     issue(lds, kbeg, s0);                                    // D(0)
@@ -837,23 +876,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     else if (t == 0 || t + 2 >= ntiles)
       vm_wait<16>();
     else
-      vm_wait<24>();
+      vm_wait<17>();
     uint8_t* cur = lds + (t & 1) * CK_STAGE + wave * 32 * 256;  // this wave's 32 rows
     const int k_valid = kend - (k0 + 32 * wave);
-    if (k_valid < 32 || bad_t0 != 0)
-      dense_tile<1, 32, true, true>(cur, cur + CK_TILE * 256, ad, qf, st, c, k_valid, bad_t0);
-    else
-      dense_tile<1, 32, false, true>(cur, cur + CK_TILE * 256, ad, qf, st, c, 32);
+    uint64_t badk = bad_t0;
+    if (k_valid < 32) badk |= k_valid <= 0 ? 0xffffffffull : (0xffffffffull << k_valid) & 0xffffffffull;
+    cached_tile(cur, cur + CK_TILE * 256, ad, qf, st, c, badk);
     uint32_t bad_t2 = 0;
     if (t + 2 < ntiles) {
       // this wave's rows of stage t&1 are free again: issue D(t+2) there,
-      // after S(t+3) (slot_ahead holds S(t+2), landed behind D(t+1))
+      // after S(t+3) (S(t+2) landed behind D(t+1))
       vm_wait<16>();  // S(t+2); D(t+1) may stay in flight
-      slots_ready(slot_ahead);
       int cur_slots[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) cur_slots[j] = slot_ahead[j];
-      if (t + 3 < ntiles) fetch_slots(slot_ahead, k0 + 3 * CK_TILE);
+      read_slots(t + 2, cur_slots);
+      if (t + 3 < ntiles) fetch_slots(t + 3);
       bad_t2 = invalid_rows(k0 + 2 * CK_TILE, cur_slots);
       issue(lds + (t & 1) * CK_STAGE, k0 + 2 * CK_TILE, cur_slots);
     }
@@ -863,6 +899,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   cached_merge_store(a, lds, st, s, hkv, mt, split, qrow0, M, m_base, g);
 }
 
+// ---------------------------------------------------------------------------
+// K3b, register-staged form: NW wavefronts over RB row blocks of 32 M rows of
+// one (segment, KV head); the KG = NW / RB wavefronts of a row block split
+// every tile of 32 * KG keys, 32 keys each.  A wavefront loads the K rows of
+// its 32 keys straight into registers -- lane l's eight 16-byte pieces (row
+// l % 32, d = 16 kk + 8 (l / 32)) are exactly its A-operand fragments of
+// S^T = K Q^T -- and DMAs their V rows into its own 8 KiB LDS stage.  With K
+// out of LDS a wavefront keeps ST tiles in flight (K in ST register buffers,
+// V in ST stages) instead of two, and never waits for another wavefront
+// until the final merge.  The Q rows go through LDS once and every
+// wavefront reads its Q^T fragments from there at each tile.
+//
+// Per wavefront the vector-memory operations are issued in this order:
+//   slots S(0) .. S(ST+1), Q rows, [full wait]  I(0) .. I(ST-1),
+//   then after computing tile t:  I(t+ST) (when it exists), S(t+ST+2)
+// where I(t) = K of tile t (8 loads) + V of tile t (8 DMA) and S(t) is the
+// lane's slot of tile t (fetched for every t, clamped to a valid entry).
+// They complete in order, so I(t) has landed once at most
+// 16 * min(ST-1, ntiles-1-t) + (t >= ST ? ST : 0) newer operations are
+// outstanding, and S(t+ST) once at most 17 are.
 // Merge the n_split partial records of every (segment, head, M row).
 // grid: (n_seg*Hkv*mtiles*32) rows / 2 per block; block 256 = 2 rows x 128 d.
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
@@ -1021,7 +1077,7 @@ static int block_cached_plan(int n_seg, int max_q, int max_keys, int Hq, int Hkv
   const int g = Hq / Hkv;
   mtiles = (max_q * g + 31) / 32;
   const int64_t pairs = (int64_t)n_seg * Hkv * mtiles;
-  // Aim for one workgroup per CU (256 CUs; the kernel's 128 KiB of LDS allow
+  // Aim for one workgroup per CU (256 CUs; the kernel's 132 KiB of LDS allow
   // only one) with at least two 128-key tiles per split.  More splits would
   // run as a second generation of workgroups plus the combine launch: 8 x 32
   // rows against 288 cached rows took 36 us with 512 workgroups, 17 us with 256.
@@ -1095,12 +1151,12 @@ static int block_cached_impl(const char* name, const dllm_bf16* q, const dllm_bf
   a.xcd_chunk = (int)(per_pair < 16 ? per_pair : 16);
   const int64_t grain = 8 * (int64_t)a.xcd_chunk;
   const int nb = (int)((logical + grain - 1) / grain * grain);
-  constexpr int lds_bytes = 2 * CK_STAGE;
+  constexpr int lds_bytes = 2 * CK_STAGE + 4 * 4 * 64 * 4;  // two stages, the slot ring
   if ((rc = set_lds(attn_cached_kernel, lds_bytes, name))) return rc;
   attn_cached_kernel<<<dim3(nb), dim3(256), lds_bytes, st>>>(a);
   if ((rc = check_launch(name))) return rc;
   if (n_split > 1) {
-    const int64_t rows = (int64_t)n_seg * Hkv * mtiles * 32;
+    const int64_t rows = (int64_t)n_seg * Hkv * a.mtiles * 32;
     attn_combine_kernel<<<dim3((unsigned)((rows + 1) / 2)), dim3(256), 0, st>>>(a);
     if ((rc = check_launch(name))) return rc;
   }

@@ -5,8 +5,8 @@
 //
 // Four launches per call:
 //   1. qbar_kernel   block mean of q per (job, query head): the block rows
-//                    are staged through LDS in one batch and summed in f64,
-//                    rows in order.
+//                    are staged through LDS and summed in f64, rows in
+//                    order, one thread per two d.
 //   2. score_kernel  per (job, KV head, 256 candidates): the candidates' K
 //                    rows of that head are loaded coalesced into LDS, then
 //                    each lane computes its candidate's dot products with
@@ -126,45 +126,46 @@ __device__ int block_excount(bool flag, int* wave_tot, int* total) {
 }
 
 // ---- 1. block mean of q ------------------------------------------------------
-// grid (n_job, Hq), block 256: qbar[j][h][d] = bf16(f32(f64 sum_t q[bs+t][h][d] / bl)),
-// t ascending.  Rows go through LDS kQbarRows at a time (one load each per
-// thread, all in flight together); 16 threads then sum 8 d each.
+// grid (n_job, ceil(Hq / 4)), block 256 = 4 query heads x 64 threads:
+// qbar[j][h][d] = bf16(f32(f64 sum_t q[bs+t][h][d] / bl)), t ascending.  The
+// block rows of the 4 heads go through LDS kQbarRows at a time (every load of
+// a round in flight together); thread (head, l) then sums d = 2l and 2l + 1
+// row by row (64 lanes read 64 consecutive words: no bank conflicts).
+constexpr int kQbarHeads = 4;
 __global__ __launch_bounds__(256) void qbar_kernel(SelArgs a) {
-  __shared__ u32x4_t tile[kQbarRows * 16];
+  __shared__ uint32_t tile[kQbarRows * kQbarHeads * 64];  // [row][head][64 words]
   const int jid = blockIdx.x;
-  const int h = blockIdx.y;
+  const int h0 = blockIdx.y * kQbarHeads;
   const Job jb = load_job(a, jid);
   if (jb.n_keep <= 0) return;
   const int tid = threadIdx.x;
-  const int rsub = tid >> 4, ch = tid & 15;
-  const uint16_t* q0 = a.q + ((int64_t)jb.row0 + jb.bs) * a.q_stride + (int64_t)h * SHD;
-  double acc[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) acc[e] = 0.0;
+  const int hh = tid >> 6, l = tid & 63;
+  const uint16_t* q0 = a.q + ((int64_t)jb.row0 + jb.bs) * a.q_stride + (int64_t)h0 * SHD;
+  double s0 = 0.0, s1 = 0.0;
   for (int t0 = 0; t0 < jb.bl; t0 += kQbarRows) {
     const int n = min(kQbarRows, jb.bl - t0);
-#pragma unroll
-    for (int p = 0; p < kQbarRows / 16; ++p) {
-      const int r = 16 * p + rsub;
-      if (r < n) tile[r * 16 + ch] = ld128(q0 + (int64_t)(t0 + r) * a.q_stride + ch * 8);
+    // load: 16-byte chunk ch of (row r, head hl): 64 chunks per row, 4 rows per pass
+    for (int i = tid; i < n * kQbarHeads * 16; i += blockDim.x) {
+      const int r = i / (kQbarHeads * 16), rem = i - r * (kQbarHeads * 16);
+      const int hl = rem >> 4, ch = rem & 15;
+      if (h0 + hl < a.Hq)
+        *reinterpret_cast<u32x4_t*>(tile + (r * kQbarHeads + hl) * 64 + ch * 4) =
+            ld128(q0 + (int64_t)(t0 + r) * a.q_stride + hl * SHD + ch * 8);
     }
     __syncthreads();
-    if (tid < 16) {
+    if (h0 + hh < a.Hq) {
       for (int r = 0; r < n; ++r) {
-        const u32x4_t x = tile[r * 16 + tid];
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          acc[2 * w] += (double)bf16_val(x[w] & 0xffffu);
-          acc[2 * w + 1] += (double)bf16_val(x[w] >> 16);
-        }
+        const uint32_t w = tile[(r * kQbarHeads + hh) * 64 + l];
+        s0 += (double)bf16_val(w & 0xffffu);
+        s1 += (double)bf16_val(w >> 16);
       }
     }
     __syncthreads();
   }
-  if (tid < 16) {
-    uint16_t* out = a.qbar + ((int64_t)jid * a.Hq + h) * SHD + tid * 8;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) out[e] = (uint16_t)f64_to_bf16_bits_2step(acc[e] / (double)jb.bl);
+  if (h0 + hh < a.Hq) {
+    uint16_t* out = a.qbar + ((int64_t)jid * a.Hq + h0 + hh) * SHD + 2 * l;
+    out[0] = (uint16_t)f64_to_bf16_bits_2step(s0 / (double)jb.bl);
+    out[1] = (uint16_t)f64_to_bf16_bits_2step(s1 / (double)jb.bl);
   }
 }
 
@@ -233,17 +234,6 @@ __global__ __launch_bounds__(256) void score_kernel(SelArgs a) {
 }
 
 // ---- 3. top-k ------------------------------------------------------------------
-// Raw score of candidate u before the division by sqrt(D): the stored group
-// maximum (head_select), or bf16 of the KV heads' partial sums added in head
-// order (token selection).
-__device__ __forceinline__ float raw_score(const SelArgs& a, const Job& jb, int jid, int h, int u) {
-  if (jb.head_select) return bf16_val(a.raw[((int64_t)jid * a.Hkv + h) * a.max_kc + u]);
-  double t = 0.0;
-  const double* p = a.part + (int64_t)jid * a.Hkv * a.max_kc + u;
-  for (int kv = 0; kv < a.Hkv; ++kv) t += p[(int64_t)kv * a.max_kc];
-  return bf16_val(f64_to_bf16_bits_2step(t));
-}
-
 // Bitonic sort, descending, of n (a power of two) unique 64-bit keys in LDS.
 __device__ void bitonic_desc_u64(uint64_t* keys, int n) {
   for (int kk = 2; kk <= n; kk <<= 1) {
@@ -289,7 +279,7 @@ struct TopkShared {
   int running[256];
   int wave_tot[16];
   uint32_t chunk[kTopkThreads];
-  int misc[4];
+  int misc[4];  // threshold search results: high byte, count above it, low byte, count above T
 };
 
 // One stable counting pass of the large-sort path: elements [0, n) of
@@ -340,9 +330,87 @@ __device__ void radix_pass(TopkShared& sh, const uint16_t* in_key, const int32_t
   }
 }
 
+// Threshold bin of a 256-bin histogram: the bin b, scanning from 255 down,
+// where cum0 + count(bins above b) < nk <= cum0 + count(bins >= b).  Wavefront
+// 0 searches (lane l holds bins 255-4l .. 252-4l and a prefix scan over the
+// lanes gives each its count above); out[0] = b, out[1] = cum0 + count above b.
+// The caller must hold a barrier before (hist complete) and after (out read).
+__device__ void find_bin(const uint32_t* hist, int nk, int cum0, int* out) {
+  if (threadIdx.x >= 64) return;
+  const int lane = threadIdx.x;
+  int h[4], own = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    h[i] = (int)hist[255 - 4 * lane - i];
+    own += h[i];
+  }
+  int incl = own;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(incl, off);
+    if (lane >= off) incl += y;
+  }
+  int run = cum0 + incl - own, hit = -1, hit_run = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if (hit < 0 && run + h[i] >= nk) {
+      hit = 255 - 4 * lane - i;
+      hit_run = run;
+    }
+    run += h[i];
+  }
+  const uint64_t m = __builtin_amdgcn_ballot_w64(hit >= 0);
+  const int first = m ? __builtin_ctzll(m) : 63;   // the lane holding the highest such bin
+  if (lane == first) {
+    out[0] = hit >= 0 ? hit : 0;
+    out[1] = hit >= 0 ? hit_run : cum0;
+  }
+}
+
+// Bitonic sort, descending, of one 32-bit value per thread over the first n
+// threads (n a power of two <= 1024; the other threads hold values sorted
+// among themselves).  Strides below 64 exchange within the wavefront by
+// lane permutes; larger ones go through `xchg` (1024 words of LDS).
+__device__ uint32_t bitonic_desc_reg(uint32_t x, int n, uint32_t* xchg) {
+  const int p = threadIdx.x;
+  for (int kk = 2; kk <= n; kk <<= 1) {
+    for (int jj = kk >> 1; jj > 0; jj >>= 1) {
+      uint32_t y;
+      if (jj >= 64) {
+        __syncthreads();
+        xchg[p] = x;
+        __syncthreads();
+        y = xchg[p ^ jj];
+      } else {
+        y = (uint32_t)__shfl_xor((int)x, jj);
+      }
+      const bool low = (p & jj) == 0, desc = (p & kk) == 0;
+      x = (low == desc) ? max(x, y) : min(x, y);
+    }
+  }
+  return x;
+}
+
+constexpr int kLdsCand = 16384;  // candidates whose raw scores and order keys stay in LDS
+constexpr int kRegSort = 1024;   // selected rows sorted one per thread in registers
+
+// bf16 bits of the raw score of candidate u before the division by sqrt(D): the
+// stored group maximum (head_select), or bf16 of the KV heads' partial sums added
+// in head order (token selection)
+__device__ __forceinline__ uint16_t raw_bits(const SelArgs& a, const Job& jb, int jid, int h, int u) {
+  if (jb.head_select) return a.raw[((int64_t)jid * a.Hkv + h) * a.max_kc + u];
+  double t = 0.0;
+  const double* p = a.part + (int64_t)jid * a.Hkv * a.max_kc + u;
+  for (int kv = 0; kv < a.Hkv; ++kv) t += p[(int64_t)kv * a.max_kc];
+  return (uint16_t)f64_to_bf16_bits_2step(t);
+}
+
 // grid (Hkv, n_job), block 1024.  Token-selection jobs use selection head 0 only.
+// LDS: 128 KiB pool (small path: raw bits, order keys and 32-bit sort keys of
+// up to kLdsCand candidates; large path: kSortCap 64-bit sort keys) + the
+// shared scratch.
 __global__ __launch_bounds__(kTopkThreads) void topk_kernel(SelArgs a) {
-  __shared__ uint64_t skey[kSortCap];
+  __shared__ __attribute__((aligned(16))) uint8_t pool[128 * 1024];
   __shared__ TopkShared sh;
   const int h = blockIdx.x;
   const int jid = blockIdx.y;
@@ -353,41 +421,119 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(SelArgs a) {
   const int tid = threadIdx.x;
   const int64_t base = ((int64_t)jid * a.Hkv + h) * a.max_kc;
   const int64_t sbase = ((int64_t)jid * a.Hkv + h) * a.max_keep;
-  uint16_t* ok = a.okey + base;
-
-  // pooled, scaled order keys: max over the window clipped to the candidates,
-  // then bf16(f32 / f32(sqrt D)) (monotone, so pooling before or after the
-  // division gives the same value)
   const int pk = jb.pool_k;
   const int pad = pk / 2;
+  int64_t* io = a.idx_out ? a.idx_out + sbase : nullptr;
+  int32_t* so = a.sel + sbase;
+  for (int b = tid; b < 256; b += blockDim.x) sh.hist[b] = 0;
+
+  if (kc <= kLdsCand) {
+    // ---- small path: everything in LDS -------------------------------------
+    uint16_t* rawl = reinterpret_cast<uint16_t*>(pool);
+    uint16_t* okl = rawl + kLdsCand;
+    uint32_t* skey = reinterpret_cast<uint32_t*>(pool + 64 * 1024);
+    for (int c = tid; c < kc; c += blockDim.x) rawl[c] = raw_bits(a, jb, jid, h, c);
+    __syncthreads();
+    // pooled, scaled order keys (max over the window clipped to the
+    // candidates, then bf16(f32 / f32(sqrt D)): monotone, so pooling before
+    // or after the division gives the same value) and the high-byte histogram
+    for (int c = tid; c < kc; c += blockDim.x) {
+      const int lo = pk > 1 ? max(0, c - pad) : c;
+      const int hi = pk > 1 ? min(kc - 1, c - pad + pk - 1) : c;
+      float m = -INFINITY;
+      for (int u = lo; u <= hi; ++u) m = fmaxf(m, bf16_val(rawl[u]));
+      const uint32_t key = bf16_order_key(f32_to_bf16_bits(m / a.sqrt_d));
+      okl[c] = (uint16_t)key;
+      atomicAdd(&sh.hist[key >> 8], 1u);
+    }
+    __syncthreads();
+    find_bin(sh.hist, nk, 0, sh.misc);
+    __syncthreads();
+    const uint32_t hb = (uint32_t)sh.misc[0];
+    const int above_hb = sh.misc[1];
+    for (int b = tid; b < 256; b += blockDim.x) sh.hist[b] = 0;
+    __syncthreads();
+    for (int c = tid; c < kc; c += blockDim.x) {
+      const uint32_t key = okl[c];
+      if ((key >> 8) == hb) atomicAdd(&sh.hist[key & 255], 1u);
+    }
+    __syncthreads();
+    find_bin(sh.hist, nk, above_hb, sh.misc + 2);
+    __syncthreads();
+    const uint32_t T = (hb << 8) | (uint32_t)sh.misc[2];
+    const int need_eq = nk - sh.misc[3];  // ties at T to take, lowest indices first
+    // index-order compaction; unique keys: score key, then the complement of the candidate
+    int run_eq = 0, run_pos = 0;
+    for (int b0 = 0; b0 < kc; b0 += kTopkThreads) {
+      const int c = b0 + tid;
+      const uint32_t key = c < kc ? okl[c] : 0u;
+      const bool gt = c < kc && key > T;
+      const bool eq = c < kc && key == T;
+      int eq_tot, sel_tot;
+      const int er = block_excount(eq, sh.wave_tot, &eq_tot) + run_eq;
+      const bool take = gt || (eq && er < need_eq);
+      const int pos = block_excount(take, sh.wave_tot, &sel_tot) + run_pos;
+      if (take) skey[pos] = (key << 16) | (uint32_t)(0xffff - c);
+      run_eq += eq_tot;
+      run_pos += sel_tot;
+    }
+    int P2 = 1;
+    while (P2 < nk) P2 <<= 1;
+    __syncthreads();
+    if (P2 <= kRegSort) {
+      uint32_t x = tid < nk ? skey[tid] : 0u;  // 0 sorts below every real key
+      x = bitonic_desc_reg(x, P2, sh.chunk);
+      if (tid < nk) {
+        const int c = 0xffff - (int)(x & 0xffffu);
+        so[tid] = c;
+        if (io) io[tid] = c;
+      }
+    } else {
+      for (int i = nk + tid; i < P2; i += blockDim.x) skey[i] = 0u;
+      __syncthreads();
+      for (int kk = 2; kk <= P2; kk <<= 1) {
+        for (int jj = kk >> 1; jj > 0; jj >>= 1) {
+          for (int i = tid; i < P2; i += blockDim.x) {
+            const int ixj = i ^ jj;
+            if (ixj > i) {
+              const uint32_t x = skey[i], y = skey[ixj];
+              const bool desc = (i & kk) == 0;
+              if (desc ? (x < y) : (x > y)) {
+                skey[i] = y;
+                skey[ixj] = x;
+              }
+            }
+          }
+          __syncthreads();
+        }
+      }
+      for (int r = tid; r < nk; r += blockDim.x) {
+        const int c = 0xffff - (int)(skey[r] & 0xffffu);
+        so[r] = c;
+        if (io) io[r] = c;
+      }
+    }
+    return;
+  }
+
+  // ---- large path: order keys in the workspace -------------------------------
+  uint64_t* skey = reinterpret_cast<uint64_t*>(pool);
+  uint16_t* ok = a.okey + base;
+  __syncthreads();
   for (int c = tid; c < kc; c += blockDim.x) {
     const int lo = pk > 1 ? max(0, c - pad) : c;
     const int hi = pk > 1 ? min(kc - 1, c - pad + pk - 1) : c;
     float m = -INFINITY;
-    for (int u = lo; u <= hi; ++u) m = fmaxf(m, raw_score(a, jb, jid, h, u));
-    ok[c] = (uint16_t)bf16_order_key(f32_to_bf16_bits(m / a.sqrt_d));
+    for (int u = lo; u <= hi; ++u) m = fmaxf(m, bf16_val(raw_bits(a, jb, jid, h, u)));
+    const uint32_t key = bf16_order_key(f32_to_bf16_bits(m / a.sqrt_d));
+    ok[c] = (uint16_t)key;
+    atomicAdd(&sh.hist[key >> 8], 1u);
   }
-  __syncthreads();  // the workgroup's own global writes, read back below
-
-  // threshold key T: count(key > T) < nk <= count(key >= T), by the high byte
-  // then the low byte
-  for (int b = tid; b < 256; b += blockDim.x) sh.hist[b] = 0;
-  __syncthreads();
-  for (int c = tid; c < kc; c += blockDim.x) atomicAdd(&sh.hist[ok[c] >> 8], 1u);
-  __syncthreads();
-  if (tid == 0) {
-    int cum = 0, b = 255;
-    for (; b > 0; --b) {
-      if (cum + (int)sh.hist[b] >= nk) break;
-      cum += (int)sh.hist[b];
-    }
-    sh.misc[0] = b;
-    sh.misc[1] = cum;
-  }
+  __syncthreads();  // also makes the workgroup's own global writes visible to it
+  find_bin(sh.hist, nk, 0, sh.misc);
   __syncthreads();
   const uint32_t hb = (uint32_t)sh.misc[0];
   const int above_hb = sh.misc[1];
-  __syncthreads();
   for (int b = tid; b < 256; b += blockDim.x) sh.hist[b] = 0;
   __syncthreads();
   for (int c = tid; c < kc; c += blockDim.x) {
@@ -395,18 +541,10 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(SelArgs a) {
     if ((key >> 8) == hb) atomicAdd(&sh.hist[key & 255], 1u);
   }
   __syncthreads();
-  if (tid == 0) {
-    int cum = above_hb, b = 255;
-    for (; b > 0; --b) {
-      if (cum + (int)sh.hist[b] >= nk) break;
-      cum += (int)sh.hist[b];
-    }
-    sh.misc[2] = (int)((hb << 8) | (uint32_t)b);
-    sh.misc[3] = nk - cum;  // ties at T to take, lowest indices first
-  }
+  find_bin(sh.hist, nk, above_hb, sh.misc + 2);
   __syncthreads();
-  const uint32_t T = (uint32_t)sh.misc[2];
-  const int need_eq = sh.misc[3];
+  const uint32_t T = (hb << 8) | (uint32_t)sh.misc[2];
+  const int need_eq = nk - sh.misc[3];
   const bool small = nk <= kSortCap;
 
   // index-order compaction of the selected candidates
@@ -431,8 +569,6 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(SelArgs a) {
     run_eq += eq_tot;
     run_pos += sel_tot;
   }
-  int64_t* io = a.idx_out ? a.idx_out + sbase : nullptr;
-  int32_t* so = a.sel + sbase;
   if (small) {
     int P2 = 1;
     while (P2 < nk) P2 <<= 1;
@@ -561,7 +697,7 @@ extern "C" int dllm_select_kv_store(const dllm_bf16* q, const dllm_bf16* k, cons
     a.cidx1 = reinterpret_cast<int32_t*>(ws + o); o += L.cidx;
   }
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  qbar_kernel<<<dim3(n_job, Hq), dim3(256), 0, st>>>(a);
+  qbar_kernel<<<dim3(n_job, (Hq + kQbarHeads - 1) / kQbarHeads), dim3(256), 0, st>>>(a);
   int rc = check_launch(name);
   if (rc) return rc;
   const size_t score_lds = (size_t)kScoreCands * 256 + (size_t)a.g * SHD * sizeof(float);

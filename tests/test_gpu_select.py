@@ -114,6 +114,7 @@ def test_select_store_bit_exact(dev, n_tok, bs, bl, Hq, Hkv, ratio, head_select,
     (12352, 12288, 64, 8, 8, 0.5, True, 3),    # 12288 candidates, 6144 kept: compaction, then the LDS sort
     (12352, 6000, 64, 8, 4, 0.5, False, 3),    # the same with GQA token selection
     (20032, 20000, 32, 4, 4, 0.9, True, 3),    # 18000 kept: the two-pass radix sort in the workspace
+    (20032, 5000, 32, 4, 4, 0.3, True, 3),     # keys in the workspace, 6000 kept: 64-bit keys sorted in LDS
     (20032, 100, 32, 4, 2, 0.75, False, 1),    # 15000 kept, token selection, no pooling
 ])
 def test_select_beyond_8192_candidates(dev, n_tok, bs, bl, Hq, Hkv, ratio, head_select, pool_k):

@@ -119,6 +119,13 @@ __device__ __forceinline__ void vm_wait() {
   asm volatile("" ::: "memory");
 }
 
+// Workgroup barrier between wavefronts that each waited for their own DMA
+// (vm_wait) and finished their own LDS reads: the wait on LDS reads plus
+// s_barrier is all the ordering needed.  __syncthreads() in a kernel that
+// fills LDS with global_load_lds makes the compiler wait for vmcnt(0) before
+// the barrier, which would also retire the DMA of the next tile.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // AUX = 2: non-temporal (streaming) policy, for bytes that one workgroup reads once.
 template <int AUX = 0>
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint8_t* lds_dst, uint32_t voff) {
@@ -566,6 +573,15 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(OCC, OC
 // softmax.
 constexpr int CK_TILE = 128;
 constexpr int CK_STAGE = 2 * CK_TILE * 256;
+constexpr int CK_MERGE_LD = 34;
+constexpr int CK_MERGE_BYTES = (8 * 32 + 4 * HD * CK_MERGE_LD) * 4;  // one row block's merge area
+static_assert(CK_MERGE_BYTES <= 2 * CK_STAGE, "a merge area fits in the two stages");
+// LDS of the kernel with RB row blocks: two stages, the slot ring
+// ([4 tiles][4 RB wavefronts][64] words), or RB merge areas if larger
+constexpr int ck_lds_bytes(int rb) {
+  return 2 * CK_STAGE + 4 * 4 * rb * 64 * 4 > rb * CK_MERGE_BYTES ? 2 * CK_STAGE + 4 * 4 * rb * 64 * 4
+                                                                  : rb * CK_MERGE_BYTES;
+}
 
 // Cache and block rows of a segment are read by exactly one workgroup, each
 // 16-byte piece by one lane of one DMA instruction: streaming loads (the q
@@ -575,13 +591,15 @@ __device__ __forceinline__ void gdma16(const void* g, uint8_t* lds_dst) {
   __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds_dst, 16, 0, kStreamAux);
 }
 
-// The four wavefronts' softmax states of one workgroup (each holds the same
-// 32 M rows over its own keys) merged in LDS, normalised and written to o --
-// or, when the keys are split across workgroups, written as a partial record
-// for attn_combine_kernel.  Every thread of the workgroup calls it once.
+// The four wavefronts' softmax states of one row block (each holds the same
+// 32 M rows over its own keys) merged in LDS at `lds`, normalised and written
+// to o -- or, when the keys are split across workgroups, written as a partial
+// record for attn_combine_kernel.  Every thread of the workgroup calls it
+// once (it holds workgroup barriers); `tid` is the thread's index within its
+// row block's 256 threads.
 __device__ __forceinline__ void cached_merge_store(const AttnArgs& a, uint8_t* lds, const DenseState<1>& st, int s,
-                                                   int hkv, int mt, int split, int qrow0, int M, int m_base, int g) {
-  const int tid = threadIdx.x;
+                                                   int hkv, int mt, int split, int qrow0, int M, int m_base, int g,
+                                                   int tid) {
   const int wave = tid >> 6;
   const int lane = tid & 63;
   const int lrow = lane & 31;
@@ -593,8 +611,7 @@ __device__ __forceinline__ void cached_merge_store(const AttnArgs& a, uint8_t* l
   // below has lanes 0..31 on rows q = 0..31 of one d and lanes 32..63 on
   // d + 16, i.e. 16 * kMergeLd floats further, which puts the two halves on
   // disjoint banks (a 32-float pitch would put all of them on the same ones).
-  constexpr int kMergeLd = 34;
-  static_assert((8 * 32 + 4 * HD * kMergeLd) * 4 <= 2 * CK_STAGE, "the merge area fits in the two stages");
+  constexpr int kMergeLd = CK_MERGE_LD;
   const float m_run = st.m_run[0];
   const float l_tot = pair_sum32(st.l_run[0]);
   float* red = reinterpret_cast<float*>(lds);
@@ -710,18 +727,29 @@ __device__ __forceinline__ void cached_tile(const uint8_t* Ks, const uint8_t* Vs
     }
 }
 
+// RB row blocks of 32 M rows of one (segment, KV head) per workgroup, four
+// wavefronts each: wavefront w + 4 r computes keys 32 w .. 32 w + 31 of every
+// tile for row block r.  With RB = 1 a wavefront DMAs exactly the 32 rows it
+// computes and never waits for another one until the merge.  With RB = 2 the
+// two row blocks share every tile -- each K/V row is fetched once for 64 M
+// rows -- and wavefront w + 4 r DMAs half of those 32 rows (instructions
+// 4 r .. 4 r + 3); a workgroup barrier after the wait makes a tile visible
+// to both, and one before a stage is refilled retires its last readers.
 // Two wavefronts per SIMD as the register budget: the whole state then stays
 // in VGPRs (with a budget of 512 the compiler moves the O^T accumulators
 // between AGPRs and VGPRs around every softmax rescale).
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_cached_kernel(AttnArgs a) {
+template <int RB>
+__global__ __launch_bounds__(256 * RB) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_cached_kernel(AttnArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  constexpr int NJ = 8 / RB;  // K (and V) DMA instructions per wavefront per tile
   const int L = xcd_remap(blockIdx.x, a.xcd_chunk);
   if (L >= a.logical_blocks) return;
+  const int mblocks = (a.mtiles + RB - 1) / RB;
   int r = L;
   const int split = r % a.n_split;
   r /= a.n_split;
-  const int mt = r % a.mtiles;
-  r /= a.mtiles;
+  const int mb = r % mblocks;
+  r /= mblocks;
   const int hkv = r % a.Hkv;
   const int s = r / a.Hkv;
   const int sid = a.seg_ids ? a.seg_ids[s] : s;
@@ -731,21 +759,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int n_c = a.slot_off[s + 1] - slot_base;
   const int g = a.g;
   const int M = Lq * g;
-  const int m_base = mt * 32;
-  if (m_base >= M) return;
+  if (mb * RB * 32 >= M) return;  // the whole workgroup: no live row block
   const int Lk = n_c + Lq;
   const int kbeg = min(split * a.keys_per_split, Lk);
   const int kend = min(Lk, kbeg + a.keys_per_split);
 
   const int tid = threadIdx.x;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wave_id = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wave = wave_id & 3;     // key block of the tile
+  const int rblk = wave_id >> 2;    // row block
+  const int mt = mb * RB + rblk;
+  const int m_base = mt * 32;
+  const int jb = rblk * NJ;         // first DMA instruction of this wavefront
   const int lane = tid & 63;
   const int lrow = lane & 31;
   const int hl = lane >> 5;
   const int rl = lane >> 4, P = lane & 15;
 
-  // ---- per-lane DMA geometry: instruction j of this wave covers tile rows
-  // 32 wave + 4j + rl; K chunk (P ^ rl) ^ 4(j & 3), V chunk P ^ 4 rl.
+  // ---- per-lane DMA geometry: instruction j of key block w covers tile rows
+  // 32 w + 4j + rl; K chunk (P ^ rl) ^ 4(j & 3), V chunk P ^ 4 rl.
   const uint32_t kchunk = (uint32_t)((P ^ rl) * 16);
   const uint32_t vchunk = (uint32_t)((P ^ (4 * rl)) * 16);
   const int64_t row_elems = (int64_t)a.Hkv * HD;
@@ -753,30 +785,28 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // outside it: the fetches then read slot_off[0], a valid dummy
   const bool have_slots = n_c > 0 && a.slots != nullptr && a.cache_slots > 0;
   const int32_t* sp = have_slots ? a.slots + slot_base : a.slot_off;
-  // Per-wave pipeline (a wavefront DMAs and reads only its own 32 rows of a
-  // tile, so no workgroup barrier is needed until the merge): the slots of
-  // tile t+2 are fetched before tile t+1's DMA is issued, so that after
-  // computing tile t the wave can issue tile t+2 into the stage it just
-  // freed while tile t+1 is still in flight -- two tiles in flight per wave.
-  // Vector memory operations complete in issue order, so each wait is "at
-  // most N newer operations outstanding": a tile is 16 DMA instructions, a
-  // slot fetch one.
-  // The slots arrive by DMA too (lane l: the slot of key 32 wave + l of the
+  // Per-wave pipeline: the slots of tile t+2 are fetched before tile t+1's
+  // DMA is issued, so that after computing tile t the wave can issue tile
+  // t+2 into the stage it just freed while tile t+1 is still in flight --
+  // two tiles in flight.  Vector memory operations complete in issue order,
+  // so each wait is "at most N newer operations outstanding": a tile is
+  // 2 NJ DMA instructions, a slot fetch one.
+  // The slots arrive by DMA too (lane l: the slot of key 32 w + l of the
   // tile) into a ring of four per-wave entries behind the stages, and lanes
   // read them from LDS after the wait that retires the fetch: no register is
   // ever written by a load the compiler does not know about.
-  uint32_t* slot_ring = reinterpret_cast<uint32_t*>(lds + 2 * CK_STAGE);  // [4 tiles][4 waves][64]
+  uint32_t* slot_ring = reinterpret_cast<uint32_t*>(lds + 2 * CK_STAGE);  // [4 tiles][4 RB waves][64]
   auto fetch_slots = [&](int t) {
     const int kidx = kbeg + t * CK_TILE + 32 * wave + lrow;
     const int32_t* src = have_slots ? sp + min(max(kidx, 0), n_c - 1) : sp;
-    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(slot_ring + ((t & 3) * 4 + wave) * 64),
-                                     4, 0, 0);
+    __builtin_amdgcn_global_load_lds(
+        src, (__attribute__((address_space(3))) void*)(slot_ring + ((t & 3) * 4 * RB + wave_id) * 64), 4, 0, 0);
   };
-  // this lane's slots of tile t (rows 4j + rl of the wave's 32); call after the wait
-  auto read_slots = [&](int t, int (&dst)[8]) {
-    const uint32_t* e = slot_ring + ((t & 3) * 4 + wave) * 64;
+  // this lane's slots of tile t (rows 4 (jb + j) + rl of the wave's 32); call after the wait
+  auto read_slots = [&](int t, int (&dst)[NJ]) {
+    const uint32_t* e = slot_ring + ((t & 3) * 4 * RB + wave_id) * 64;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) dst[j] = (int)e[4 * j + rl];
+    for (int j = 0; j < NJ; ++j) dst[j] = (int)e[4 * (jb + j) + rl];
   };
   // Rows past kend read the last valid row; a cached row with an invalid
   // slot reads block row 0 (never the cache, which may be absent).  Both are
@@ -792,11 +822,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const uint64_t vc0 = (uint64_t)(uintptr_t)(a.v_cache + hkv * HD);
   const uint64_t kb0 = (uint64_t)(uintptr_t)(a.k + (int64_t)qrow0 * a.k_stride + hkv * HD);
   const uint64_t vb0 = (uint64_t)(uintptr_t)(a.v + (int64_t)qrow0 * a.v_stride + hkv * HD);
-  auto issue = [&](uint8_t* stage, int k0, const int (&slot)[8]) {
+  auto issue = [&](uint8_t* stage, int k0, const int (&slot)[NJ]) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int jj = 0; jj < NJ; ++jj) {
+      const int j = jb + jj;
       const int kidx = min(k0 + 32 * wave + 4 * j + rl, max(kend - 1, 0));
-      const uint32_t sl = (uint32_t)slot[j];
+      const uint32_t sl = (uint32_t)slot[jj];
       const bool cached = kidx < n_c;
       const bool use_cache = cached && sl < n_slots;
       // a cached row with an invalid slot reads block row 0 (masked later)
@@ -804,24 +835,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       const uint64_t kaddr = (use_cache ? kc0 : kb0) + (uint64_t)idx * (use_cache ? cache_row_b : kS_b);
       const uint64_t vaddr = (use_cache ? vc0 : vb0) + (uint64_t)idx * (use_cache ? cache_row_b : vS_b);
       const int q = 8 * wave + j;
-      gdma16(reinterpret_cast<const uint8_t*>(kaddr) + (kchunk ^ (uint32_t)(64 * (j & 3))), stage + q * 1024);
+      gdma16(reinterpret_cast<const uint8_t*>(kaddr) + (kchunk ^ (uint32_t)(64 * (jj & 3))), stage + q * 1024);
       gdma16(reinterpret_cast<const uint8_t*>(vaddr) + vchunk, stage + CK_TILE * 256 + q * 1024);
     }
   };
-  // rows of this wave's block whose slot is invalid, as a 32-bit mask (bit = 4j + rl)
-  auto invalid_rows = [&](int k0, const int (&slot)[8]) -> uint32_t {
-    uint32_t m = 0;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int kidx = k0 + 32 * wave + 4 * j + rl;
-      const bool bad = kidx < n_c && kidx < kend && (uint32_t)slot[j] >= n_slots;
-      const uint64_t b = __builtin_amdgcn_ballot_w64(bad);
-      // lanes 16 rl' .. 16 rl' + 15 share row 4j + rl'
-#pragma unroll
-      for (int x = 0; x < 4; ++x)
-        if ((b >> (16 * x)) & 0xffffull) m |= 1u << (4 * j + x);
-    }
-    return m;
+  // keys of this wave's block of tile t whose slot is invalid, as a 32-bit
+  // mask (bit = key within the block), from the slot ring after the wait
+  auto invalid_keys = [&](int t) -> uint32_t {
+    const int kidx = kbeg + t * CK_TILE + 32 * wave + lrow;
+    const uint32_t sl = slot_ring[((t & 3) * 4 * RB + wave_id) * 64 + lrow];
+    const bool bad = kidx < n_c && kidx < kend && sl >= n_slots;
+    return (uint32_t)__builtin_amdgcn_ballot_w64(bad);
   };
 
   // ---- prologue: the slots of the first three tiles and the Q^T fragments
@@ -846,17 +870,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     for (int kk = 0; kk < 8; ++kk) qf[0][kk] = as_bf16x8(bload(qrs, qoff + (uint32_t)kk * 32u, 0u));
   }
   const int ntiles = (kend - kbeg + CK_TILE - 1) / CK_TILE;
-  uint32_t bad_t0 = 0, bad_t1 = 0;  // invalid-row masks of tiles t and t+1
+  uint32_t bad_t0 = 0, bad_t1 = 0;  // invalid-key masks of tiles t and t+1
   vm_wait<0>();  // S(0..2) and q
-  int s0[8], s1[8];
+  int s0[NJ], s1[NJ];
   read_slots(0, s0);
   read_slots(1, s1);
   if (ntiles > 0) {
-    bad_t0 = invalid_rows(kbeg, s0);
+    bad_t0 = invalid_keys(0);
     issue(lds, kbeg, s0);                                    // D(0)
   }
   if (ntiles > 1) {
-    bad_t1 = invalid_rows(kbeg + CK_TILE, s1);
+    bad_t1 = invalid_keys(1);
     issue(lds + CK_STAGE, kbeg + CK_TILE, s1);               // D(1)
   }
 
@@ -874,51 +898,33 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     if (t + 1 >= ntiles)
       vm_wait<0>();
     else if (t == 0 || t + 2 >= ntiles)
-      vm_wait<16>();
+      vm_wait<2 * NJ>();
     else
-      vm_wait<17>();
-    uint8_t* cur = lds + (t & 1) * CK_STAGE + wave * 32 * 256;  // this wave's 32 rows
+      vm_wait<2 * NJ + 1>();
+    if constexpr (RB > 1) lds_barrier();  // every wavefront's part of D(t) has landed
+    uint8_t* cur = lds + (t & 1) * CK_STAGE + wave * 32 * 256;  // this key block's 32 rows
     const int k_valid = kend - (k0 + 32 * wave);
     uint64_t badk = bad_t0;
     if (k_valid < 32) badk |= k_valid <= 0 ? 0xffffffffull : (0xffffffffull << k_valid) & 0xffffffffull;
     cached_tile(cur, cur + CK_TILE * 256, ad, qf, st, c, badk);
     uint32_t bad_t2 = 0;
     if (t + 2 < ntiles) {
-      // this wave's rows of stage t&1 are free again: issue D(t+2) there,
-      // after S(t+3) (S(t+2) landed behind D(t+1))
-      vm_wait<16>();  // S(t+2); D(t+1) may stay in flight
-      int cur_slots[8];
+      // stage t&1 is free again (with RB > 1 once both row blocks are done
+      // with it): issue D(t+2) there, after S(t+3) (S(t+2) landed behind D(t+1))
+      if constexpr (RB > 1) lds_barrier();
+      vm_wait<2 * NJ>();  // S(t+2); D(t+1) may stay in flight
+      int cur_slots[NJ];
       read_slots(t + 2, cur_slots);
+      bad_t2 = invalid_keys(t + 2);
       if (t + 3 < ntiles) fetch_slots(t + 3);
-      bad_t2 = invalid_rows(k0 + 2 * CK_TILE, cur_slots);
       issue(lds + (t & 1) * CK_STAGE, k0 + 2 * CK_TILE, cur_slots);
     }
     bad_t0 = bad_t1;
     bad_t1 = bad_t2;
   }
-  cached_merge_store(a, lds, st, s, hkv, mt, split, qrow0, M, m_base, g);
+  cached_merge_store(a, lds + rblk * CK_MERGE_BYTES, st, s, hkv, mt, split, qrow0, M, m_base, g, tid & 255);
 }
 
-// ---------------------------------------------------------------------------
-// K3b, register-staged form: NW wavefronts over RB row blocks of 32 M rows of
-// one (segment, KV head); the KG = NW / RB wavefronts of a row block split
-// every tile of 32 * KG keys, 32 keys each.  A wavefront loads the K rows of
-// its 32 keys straight into registers -- lane l's eight 16-byte pieces (row
-// l % 32, d = 16 kk + 8 (l / 32)) are exactly its A-operand fragments of
-// S^T = K Q^T -- and DMAs their V rows into its own 8 KiB LDS stage.  With K
-// out of LDS a wavefront keeps ST tiles in flight (K in ST register buffers,
-// V in ST stages) instead of two, and never waits for another wavefront
-// until the final merge.  The Q rows go through LDS once and every
-// wavefront reads its Q^T fragments from there at each tile.
-//
-// Per wavefront the vector-memory operations are issued in this order:
-//   slots S(0) .. S(ST+1), Q rows, [full wait]  I(0) .. I(ST-1),
-//   then after computing tile t:  I(t+ST) (when it exists), S(t+ST+2)
-// where I(t) = K of tile t (8 loads) + V of tile t (8 DMA) and S(t) is the
-// lane's slot of tile t (fetched for every t, clamped to a valid entry).
-// They complete in order, so I(t) has landed once at most
-// 16 * min(ST-1, ntiles-1-t) + (t >= ST ? ST : 0) newer operations are
-// outstanding, and S(t+ST) once at most 17 are.
 // Merge the n_split partial records of every (segment, head, M row).
 // grid: (n_seg*Hkv*mtiles*32) rows / 2 per block; block 256 = 2 rows x 128 d.
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
@@ -1072,16 +1078,25 @@ extern "C" int dllm_attn_varlen_fwd(const dllm_bf16* q, const dllm_bf16* k, cons
   return check_launch(name);
 }
 
-static int block_cached_plan(int n_seg, int max_q, int max_keys, int Hq, int Hkv, int& mtiles, int& n_split,
-                             int& keys_per_split) {
+// One workgroup per CU fits (the kernel's LDS allows only one), so the plan
+// counts generations of 256 workgroups.  Row blocks per workgroup: 2 when a
+// (segment, KV head) has at least two 32-row M tiles and pairing them saves
+// a whole generation (16 segments x 4 KV heads x 7 M tiles, 28 query heads,
+// against 732 keys: 448 -> 256 workgroups, 28 -> 19.5 us); otherwise 1,
+// which streams the same bytes with twice the workgroups (4 x 32 heads x 2 M
+// tiles against 672 keys: 16.5 us, against 19.3 us paired on 128 CUs).
+// Then the keys are split, only while the splits still fit in one
+// generation (each split adds a partial record and the combine launch), with
+// at least two 128-key tiles per split.
+static int block_cached_plan(int n_seg, int max_q, int max_keys, int Hq, int Hkv, int& mtiles, int& rb,
+                             int& n_split, int& keys_per_split) {
   const int g = Hq / Hkv;
   mtiles = (max_q * g + 31) / 32;
-  const int64_t pairs = (int64_t)n_seg * Hkv * mtiles;
-  // Aim for one workgroup per CU (256 CUs; the kernel's 132 KiB of LDS allow
-  // only one) with at least two 128-key tiles per split.  More splits would
-  // run as a second generation of workgroups plus the combine launch: 8 x 32
-  // rows against 288 cached rows took 36 us with 512 workgroups, 17 us with 256.
-  int64_t want = pairs > 0 ? (256 + pairs - 1) / pairs : 1;
+  const int64_t pairs1 = (int64_t)n_seg * Hkv * mtiles;
+  const int64_t pairs2 = (int64_t)n_seg * Hkv * ((mtiles + 1) / 2);
+  rb = (mtiles >= 2 && (pairs1 + 255) / 256 > (pairs2 + 255) / 256) ? 2 : 1;
+  const int64_t pairs = rb == 2 ? pairs2 : pairs1;
+  int64_t want = pairs > 0 ? 256 / pairs : 1;
   const int max_split = max_keys > 0 ? (max_keys + 255) / 256 : 1;
   if (want > max_split) want = max_split;
   if (want < 1) want = 1;
@@ -1097,8 +1112,8 @@ static int block_cached_plan(int n_seg, int max_q, int max_keys, int Hq, int Hkv
 extern "C" size_t dllm_attn_block_cached_workspace_size(int n_seg, int max_q, int max_keys, int Hq, int Hkv, int D) {
   (void)D;
   if (n_seg <= 0 || max_q <= 0 || Hkv <= 0 || Hq <= 0 || Hq % Hkv) return 0;
-  int mtiles, n_split, kps;
-  block_cached_plan(n_seg, max_q, max_keys, Hq, Hkv, mtiles, n_split, kps);
+  int mtiles, rb, n_split, kps;
+  block_cached_plan(n_seg, max_q, max_keys, Hq, Hkv, mtiles, rb, n_split, kps);
   if (n_split <= 1) return 0;
   const size_t nrec = (size_t)n_seg * Hkv * mtiles * n_split;
   return nrec * 32 * (HD + 2) * sizeof(float);
@@ -1129,8 +1144,8 @@ static int block_cached_impl(const char* name, const dllm_bf16* q, const dllm_bf
   a.cu_q = cu; a.cu_k = cu; a.seg_ids = seg_ids; a.slots = slots; a.slot_off = slot_off;
   a.q_stride = q_stride_tok; a.k_stride = k_stride_tok; a.v_stride = v_stride_tok; a.o_stride = o_stride_tok;
   a.n_seg = n_seg; a.Hkv = Hkv; a.g = Hq / Hkv;
-  int mtiles, n_split, kps;
-  block_cached_plan(n_seg, max_q, max_keys, Hq, Hkv, mtiles, n_split, kps);
+  int mtiles, rb, n_split, kps;
+  block_cached_plan(n_seg, max_q, max_keys, Hq, Hkv, mtiles, rb, n_split, kps);
   a.mtiles = mtiles; a.n_split = n_split; a.keys_per_split = kps;
   if (n_split > 1) {
     const size_t need = dllm_attn_block_cached_workspace_size(n_seg, max_q, max_keys, Hq, Hkv, D);
@@ -1140,20 +1155,27 @@ static int block_cached_impl(const char* name, const dllm_bf16* q, const dllm_bf
     if (!aligned16(workspace)) return fail(DLLM_ERR_INVALID_ARG, "%s: workspace must be 16-byte aligned", name);
     a.ws = reinterpret_cast<float*>(workspace);
   }
-  const int64_t logical = (int64_t)n_split * mtiles * Hkv * n_seg;
+  const int mblocks = (mtiles + rb - 1) / rb;
+  const int64_t logical = (int64_t)n_split * mblocks * Hkv * n_seg;
   if (logical > (int64_t)1 << 30) return fail(DLLM_ERR_INVALID_ARG, "%s: problem too large", name);
   a.logical_blocks = (int)logical;
   a.scale_log2 = softmax_scale * kLog2e;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  // one chunk per (segment, KV head): its m-tiles and splits read the same
+  // one chunk per (segment, KV head): its row blocks and splits read the same
   // cached rows; the pairs of one segment go to all eight XCDs
-  const int64_t per_pair = (int64_t)n_split * mtiles;
+  const int64_t per_pair = (int64_t)n_split * mblocks;
   a.xcd_chunk = (int)(per_pair < 16 ? per_pair : 16);
   const int64_t grain = 8 * (int64_t)a.xcd_chunk;
   const int nb = (int)((logical + grain - 1) / grain * grain);
-  constexpr int lds_bytes = 2 * CK_STAGE + 4 * 4 * 64 * 4;  // two stages, the slot ring
-  if ((rc = set_lds(attn_cached_kernel, lds_bytes, name))) return rc;
-  attn_cached_kernel<<<dim3(nb), dim3(256), lds_bytes, st>>>(a);
+  if (rb == 2) {
+    constexpr int lds_bytes = ck_lds_bytes(2);
+    if ((rc = set_lds(attn_cached_kernel<2>, lds_bytes, name))) return rc;
+    attn_cached_kernel<2><<<dim3(nb), dim3(512), lds_bytes, st>>>(a);
+  } else {
+    constexpr int lds_bytes = ck_lds_bytes(1);
+    if ((rc = set_lds(attn_cached_kernel<1>, lds_bytes, name))) return rc;
+    attn_cached_kernel<1><<<dim3(nb), dim3(256), lds_bytes, st>>>(a);
+  }
   if ((rc = check_launch(name))) return rc;
   if (n_split > 1) {
     const int64_t rows = (int64_t)n_seg * Hkv * a.mtiles * 32;

@@ -181,6 +181,7 @@ def _cached_case(prefix, blk, Hq, Hkv, seed, page=256, extra_pages=3):
     ([5, 300], [32, 17], 28, 4),                           # Dream GQA, short block tail
     ([0, 1], [8, 3], 8, 8),                                # empty / single cached row
     ([2100 + 13 * i for i in range(32)], [32] * 32, 8, 8),  # 256 pairs: one workgroup per pair, no split
+    ([700] * 16, [32] * 16, 28, 4),                        # Dream denoise step: 448 M tiles, paired row blocks
 ])
 def test_block_cached(dev, prefix, blk, Hq, Hkv):
     print(f"block_cached prefix={prefix} blk={blk} Hq={Hq} Hkv={Hkv}", flush=True)
@@ -199,6 +200,44 @@ def test_block_cached(dev, prefix, blk, Hq, Hkv):
                                 kc.to(dev), vc.to(dev), flat_slots.to(dev),
                                 torch.tensor(slot_off, dtype=torch.int32, device=dev), D ** -0.5, ws)
     torch.cuda.synchronize()
+    kcn, vcn = to_np(kc), to_np(vc)
+    cul = cu.tolist()
+    qn, kn, vn = to_np(q), to_np(k), to_np(v)
+    for i in range(len(blk)):
+        r0, r1 = cul[i], cul[i + 1]
+        ref = oatt.block_cached(qn[r0:r1], kn[r0:r1], vn[r0:r1], kcn, vcn, slots[i], D ** -0.5, dtype=np.float32)
+        assert_attn_close(o[r0:r1], ref, f"seq {i}")
+
+
+def test_block_cached_paired_row_blocks_ragged(dev):
+    """Two 32-row blocks per workgroup (more than one generation of
+    single-block workgroups): ragged blocks of 1..32 tokens with 7 query
+    heads per KV head (2..7 M tiles, odd counts leave a workgroup's second
+    block empty), empty and short prefixes, and slots outside the cache."""
+    blk = [32, 17, 5, 1, 32, 31, 9, 32, 24, 32, 2, 32, 32, 13, 32, 28, 32, 7, 32, 32]
+    prefix = [700, 0, 1, 255, 256, 257, 900, 33, 512, 640, 3, 700, 128, 380, 777, 64, 1000, 90, 300, 450]
+    Hq, Hkv = 28, 4
+    mt = [-(-b * 7 // 32) for b in blk]
+    assert len(blk) * Hkv * max(mt) > 512, "meant for the paired launch"
+    print(f"block_cached paired row blocks: {len(blk)} segments, ragged", flush=True)
+    q, k, v, cu, kc, vc, slots = _cached_case(prefix, blk, Hq, Hkv, seed=5)
+    slots[0][3] = -1
+    slots[8][511] = kc.shape[0]
+    slots[16][500] = 2 ** 31 - 1
+    D = 128
+    slot_off = [0]
+    for s_ in slots:
+        slot_off.append(slot_off[-1] + len(s_))
+    flat = torch.tensor([x for s_ in slots for x in s_], dtype=torch.int32)
+    o = torch.full(q.shape, float("nan"), dtype=torch.bfloat16, device=dev)
+    max_keys = max(p + b for p, b in zip(prefix, blk))
+    ws_bytes = _capi.block_cached_workspace_size(len(blk), max(blk), max_keys, Hq, Hkv, D)
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev) if ws_bytes else None
+    _capi.attn_block_cached_fwd(q.to(dev), k.to(dev), v.to(dev), o, cu.to(dev), None, len(blk), max(blk), max_keys,
+                                kc.to(dev), vc.to(dev), flat.to(dev),
+                                torch.tensor(slot_off, dtype=torch.int32, device=dev), D ** -0.5, ws)
+    torch.cuda.synchronize()
+    assert not torch.isnan(o).any(), "rows left unwritten"
     kcn, vcn = to_np(kc), to_np(vc)
     cul = cu.tolist()
     qn, kn, vn = to_np(q), to_np(k), to_np(v)
@@ -276,10 +315,12 @@ def test_block_cached_xcd_interleave_covers_every_block(dev):
         assert_attn_close(o[r0:r1], ref, f"seq {i}")
 
 
-def test_block_cached_invalid_slots_are_excluded(dev):
-    """Slots outside the cache are left out of the softmax."""
-    print("block_cached invalid slots", flush=True)
-    q, k, v, cu, kc, vc, slots = _cached_case([300, 700], [32, 32], 8, 8, seed=77)
+@pytest.mark.parametrize("Hq,Hkv", [(8, 8), (16, 4)])
+def test_block_cached_invalid_slots_are_excluded(dev, Hq, Hkv):
+    """Slots outside the cache are left out of the softmax (one 32-row block
+    per (segment, KV head), and four, two per workgroup)."""
+    print(f"block_cached invalid slots Hq={Hq} Hkv={Hkv}", flush=True)
+    q, k, v, cu, kc, vc, slots = _cached_case([300, 700], [32, 32], Hq, Hkv, seed=77)
     slots[0][5] = -3
     slots[0][100] = kc.shape[0]
     slots[1][699] = 10 ** 8
@@ -288,7 +329,7 @@ def test_block_cached_invalid_slots_are_excluded(dev):
     flat = torch.tensor(slots[0] + slots[1], dtype=torch.int32)
     qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
     o = torch.zeros_like(qd)
-    ws_b = _capi.block_cached_workspace_size(2, 32, 732, 8, 8, D)
+    ws_b = _capi.block_cached_workspace_size(2, 32, 732, Hq, Hkv, D)
     ws = torch.empty(max(ws_b, 1), dtype=torch.uint8, device=dev) if ws_b else None
     _capi.attn_block_cached_fwd(qd, kd, vd, o, cu.to(dev), None, 2, 32, 732, kc.to(dev), vc.to(dev), flat.to(dev),
                                 torch.tensor(off, dtype=torch.int32, device=dev), D ** -0.5, ws)

@@ -752,17 +752,17 @@ __global__ __launch_bounds__(256 * RB) __attribute__((amdgpu_waves_per_eu(2, 2))
   r /= mblocks;
   const int hkv = r % a.Hkv;
   const int s = r / a.Hkv;
+  // The slot list of segment s needs slot_off only: its first fetches are
+  // issued before the segment's rows (cu_q, possibly behind seg_ids) are
+  // known, so that those two dependent loads overlap.
+  // (The scalar loads of the segment's offsets all come first: a load after
+  // the first DMA into LDS could no longer be a scalar one.)
+  const int slot_base = a.slot_off[s];
+  const int n_c = a.slot_off[s + 1] - slot_base;
+  const int kbeg0 = split * a.keys_per_split;  // this split's first key (past Lk: no tiles)
   const int sid = a.seg_ids ? a.seg_ids[s] : s;
   const int qrow0 = a.cu_q[sid];
   const int Lq = a.cu_q[sid + 1] - qrow0;
-  const int slot_base = a.slot_off[s];
-  const int n_c = a.slot_off[s + 1] - slot_base;
-  const int g = a.g;
-  const int M = Lq * g;
-  if (mb * RB * 32 >= M) return;  // the whole workgroup: no live row block
-  const int Lk = n_c + Lq;
-  const int kbeg = min(split * a.keys_per_split, Lk);
-  const int kend = min(Lk, kbeg + a.keys_per_split);
 
   const int tid = threadIdx.x;
   const int wave_id = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -797,7 +797,7 @@ __global__ __launch_bounds__(256 * RB) __attribute__((amdgpu_waves_per_eu(2, 2))
   // ever written by a load the compiler does not know about.
   uint32_t* slot_ring = reinterpret_cast<uint32_t*>(lds + 2 * CK_STAGE);  // [4 tiles][4 RB waves][64]
   auto fetch_slots = [&](int t) {
-    const int kidx = kbeg + t * CK_TILE + 32 * wave + lrow;
+    const int kidx = kbeg0 + t * CK_TILE + 32 * wave + lrow;
     const int32_t* src = have_slots ? sp + min(max(kidx, 0), n_c - 1) : sp;
     __builtin_amdgcn_global_load_lds(
         src, (__attribute__((address_space(3))) void*)(slot_ring + ((t & 3) * 4 * RB + wave_id) * 64), 4, 0, 0);
@@ -808,6 +808,25 @@ __global__ __launch_bounds__(256 * RB) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
     for (int j = 0; j < NJ; ++j) dst[j] = (int)e[4 * (jb + j) + rl];
   };
+  // ---- prologue: the slots of the first three tiles, then the Q^T
+  // fragments (their address needs the segment's rows); D(0) and D(1) are
+  // issued as soon as the slots have landed, with q still in flight, and a
+  // wait that retires q follows them (so the compiler's own wait tracking
+  // has no q load left to wait for inside the tile loop).  Slot fetches
+  // past the key range read a clamped, valid index and go unused.
+  fetch_slots(0);
+  fetch_slots(1);
+  fetch_slots(2);
+  asm volatile("" ::: "memory");  // the slot fetches stay the oldest operations
+  const int g = a.g;
+  const int M = Lq * g;
+  if (mb * RB * 32 >= M) {  // the whole workgroup: no live row block
+    vm_wait<0>();            // no DMA into LDS may outlive the workgroup
+    return;
+  }
+  const int Lk = n_c + Lq;
+  const int kbeg = min(kbeg0, Lk);
+  const int kend = min(Lk, kbeg + a.keys_per_split);
   // Rows past kend read the last valid row; a cached row with an invalid
   // slot reads block row 0 (never the cache, which may be absent).  Both are
   // masked out of the softmax, so only the address needs to be valid.
@@ -848,14 +867,6 @@ __global__ __launch_bounds__(256 * RB) __attribute__((amdgpu_waves_per_eu(2, 2))
     return (uint32_t)__builtin_amdgcn_ballot_w64(bad);
   };
 
-  // ---- prologue: the slots of the first three tiles and the Q^T fragments
-  // in one batch, one full wait (which also retires q for the compiler's own
-  // wait tracking, so no wait on q remains inside the tile loop), then D(0)
-  // and D(1) together: tile 1 does not wait a second round trip.  Slot
-  // fetches past the key range read a clamped, valid index and go unused.
-  fetch_slots(0);
-  fetch_slots(1);
-  fetch_slots(2);
   const int m = m_base + lrow;
   const bool m_ok = m < M;
   const int tok = m_ok ? m / g : 0;
@@ -871,7 +882,7 @@ __global__ __launch_bounds__(256 * RB) __attribute__((amdgpu_waves_per_eu(2, 2))
   }
   const int ntiles = (kend - kbeg + CK_TILE - 1) / CK_TILE;
   uint32_t bad_t0 = 0, bad_t1 = 0;  // invalid-key masks of tiles t and t+1
-  vm_wait<0>();  // S(0..2) and q
+  vm_wait<8>();  // S(0..2); the eight q loads may be outstanding
   int s0[NJ], s1[NJ];
   read_slots(0, s0);
   read_slots(1, s1);
@@ -883,6 +894,12 @@ __global__ __launch_bounds__(256 * RB) __attribute__((amdgpu_waves_per_eu(2, 2))
     bad_t1 = invalid_keys(1);
     issue(lds + CK_STAGE, kbeg + CK_TILE, s1);               // D(1)
   }
+  if (ntiles > 1)  // q has landed; D(0) and D(1) may be in flight
+    vm_wait<4 * NJ>();
+  else if (ntiles == 1)
+    vm_wait<2 * NJ>();
+  else
+    vm_wait<0>();
 
   DenseAddr ad;
   dense_addr(ad, lane, 0u, 0u);

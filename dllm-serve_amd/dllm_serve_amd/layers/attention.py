@@ -147,6 +147,10 @@ class StepLayout:
         self.max_q_cached = max((rows[i] for i in self.cached), default=0)
         self.max_keys_cached = max((rows[i] + keeps[i] for i in self.cached), default=0)
         self.total_slots = sum(keeps[i] for i in self.cached + self.jobs_idx)
+        # a launch over every sequence in batch order gets no id table: the
+        # kernels then read a segment's offsets one dependent load earlier
+        self.dense_identity = self.dense == list(range(self.n_seq))
+        self.cached_identity = self.cached == list(range(self.n_seq))
 
     def signature(self) -> tuple:
         """Everything a captured step's launches depend on."""
@@ -162,7 +166,7 @@ class StepPlan:
     ``StepPlan.from_device`` wraps tables the device-side builder wrote."""
 
     _SCALARS = ("n_seq", "total_rows", "any_skipped", "n_dense", "max_q_dense", "n_job", "max_kc", "max_keep",
-                "max_blk", "n_cached", "max_q_cached", "max_keys_cached")
+                "max_blk", "n_cached", "max_q_cached", "max_keys_cached", "dense_identity", "cached_identity")
 
     def __init__(self, context, device: torch.device, num_kv_heads: int = 0, head_dim: int = 0, num_heads: int = 0,
                  layout: StepLayout | None = None):
@@ -303,8 +307,8 @@ class Attention(nn.Module):
         Hq, Hkv, D = self.num_heads, self.num_kv_heads, self.head_dim
 
         if plan.n_dense:
-            _capi.attn_varlen_fwd(q, k, v, o, plan.cu, plan.cu, plan.dense_ids, plan.n_dense,
-                                  plan.max_q_dense, self.scale)
+            ids = None if plan.dense_identity else plan.dense_ids
+            _capi.attn_varlen_fwd(q, k, v, o, plan.cu, plan.cu, ids, plan.n_dense, plan.max_q_dense, self.scale)
 
         if plan.n_job:
             if not (self.k_cache.numel() and self.v_cache.numel()):
@@ -324,8 +328,8 @@ class Attention(nn.Module):
             self._check_cache(q.device)
             ws = plan.workspace("cached", _capi.block_cached_workspace_size(
                 plan.n_cached, plan.max_q_cached, plan.max_keys_cached, Hq, Hkv, D))
-            _capi.attn_block_cached_fwd(q, k, v, o, plan.cu, plan.cached_ids, plan.n_cached,
-                                        plan.max_q_cached, plan.max_keys_cached,
+            ids = None if plan.cached_identity else plan.cached_ids
+            _capi.attn_block_cached_fwd(q, k, v, o, plan.cu, ids, plan.n_cached, plan.max_q_cached, plan.max_keys_cached,
                                         self.k_cache, self.v_cache, plan.slots, plan.slot_off,
                                         self.scale, ws)
         return o.view(-1, Hq * D)

@@ -147,8 +147,8 @@ def bench_dense(lens, Hq, Hkv, D, n_layers, steps, warmup, dev, seed=0):
         i = state["i"] % n_layers
         state["i"] += 1
         q, k, v = layers[i]
-        _capi.attn_varlen_fwd(q, k, v, outs[i], plan.cu, plan.cu, plan.dense_ids, plan.n_dense, plan.max_q_dense,
-                              D ** -0.5)
+        _capi.attn_varlen_fwd(q, k, v, outs[i], plan.cu, plan.cu, None if plan.dense_identity else plan.dense_ids,
+                              plan.n_dense, plan.max_q_dense, D ** -0.5)
 
     ms_kernel = time_kernel(one, iters=4 * n_layers)
     # the same step's layer calls captured once in a HIP graph and replayed
@@ -228,14 +228,156 @@ def bench_copy(dev, nbytes=1 << 30):
     return dict(bytes=2.0 * nbytes, us=ms * 1e3, gbs=2.0 * nbytes / (ms * 1e-3) / 1e9)
 
 
+def _paged_slots(prefix, seed, page=256):
+    """Per-sequence slot lists over shuffled 256-row pages, and the page count."""
+    pages_per = [-(-p // page) for p in prefix]
+    n_pages = sum(pages_per) + 1
+    perm = torch.randperm(n_pages, generator=torch.Generator().manual_seed(seed)).tolist()
+    slots, at = [], 0
+    for p, npg in zip(prefix, pages_per):
+        for j in range(npg):
+            fill = page if j < npg - 1 else p - page * (npg - 1)
+            slots.extend(range(perm[at + j] * page, perm[at + j] * page + fill))
+        at += npg
+    return slots, n_pages
+
+
+# (name, segments, block rows, cached rows per segment, Hq, Hkv): the state-2
+# (reuse) steps of the denoise loops.  C4 at retention 1.0 is the same block
+# against all 1216 candidate rows.
+DENOISE_CACHED_SHAPES = (
+    ("c2_cached_8x32_vs_352", 8, 32, 352, 32, 32),
+    ("c4_reuse_4x64_vs_608", 4, 64, 608, 32, 32),
+    ("c4_ret1_4x64_vs_1216", 4, 64, 1216, 32, 32),
+    ("dream_gqa_16x32_vs_700", 16, 32, 700, 28, 4),
+)
+
+
+def bench_denoise_shapes(dev, n_layers=8):
+    """K3b (block-cached attention) at the denoise-loop reuse shapes, each
+    launch on another layer's q/k/v and cache (n_layers of them, so the cache
+    rows come from HBM, not from a previous launch's cache residue).  Bytes
+    are the algorithmic ones: Q and O of the block, K/V of block and cached
+    rows, the int32 slot list."""
+    from oracle.configs import attention_bytes, attention_flops
+    from dllm_serve_amd import _capi
+
+    D = 128
+    out = {}
+    for name, B, Lq, n_c, Hq, Hkv in DENOISE_CACHED_SHAPES:
+        prefix = [n_c] * B
+        slots, n_pages = _paged_slots(prefix, seed=1)
+        g = torch.Generator(device=dev).manual_seed(0)
+        n = B * Lq
+        layers = []
+        for _ in range(n_layers):
+            kc = torch.randn(n_pages * 256, Hkv, D, generator=g, device=dev, dtype=torch.bfloat16)
+            vc = torch.randn(n_pages * 256, Hkv, D, generator=g, device=dev, dtype=torch.bfloat16)
+            q = torch.randn(n, Hq, D, generator=g, device=dev, dtype=torch.bfloat16)
+            k = torch.randn(n, Hkv, D, generator=g, device=dev, dtype=torch.bfloat16)
+            v = torch.randn(n, Hkv, D, generator=g, device=dev, dtype=torch.bfloat16)
+            layers.append((q, k, v, torch.empty_like(q), kc, vc))
+        cu = torch.arange(0, n + 1, Lq, dtype=torch.int32, device=dev)
+        sl = torch.tensor(slots, dtype=torch.int32, device=dev)
+        so = torch.tensor([i * n_c for i in range(B + 1)], dtype=torch.int32, device=dev)
+        max_keys = n_c + Lq
+        ws_b = _capi.block_cached_workspace_size(B, Lq, max_keys, Hq, Hkv, D)
+        ws = torch.empty(max(ws_b, 16), dtype=torch.uint8, device=dev) if ws_b else None
+        state = {"i": 0}
+
+        def one():
+            q, k, v, o, kc, vc = layers[state["i"] % n_layers]
+            state["i"] += 1
+            _capi.attn_block_cached_fwd(q, k, v, o, cu, None, B, Lq, max_keys, kc, vc, sl, so, D ** -0.5, ws)
+
+        reps = [time_kernel(one, iters=8 * n_layers, settle_s=0.05 if r else 0.1) for r in range(5)]
+        ms = sorted(reps)[2]
+        byts = attention_bytes([Lq] * B, [n_c + Lq] * B, Hq, Hkv, D) + 4.0 * B * n_c
+        fl = attention_flops([Lq] * B, [n_c + Lq] * B, Hq, D)
+        out[name] = dict(kernel_us=round(ms * 1e3, 2), bytes_per_call=byts, gbs=round(byts / (ms * 1e-3) / 1e9, 1),
+                         frac_of_hbm=round(byts / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                         tflops=round(fl / (ms * 1e-3) / 1e12, 1))
+        del layers
+    out["c4_ret1_over_reuse_kernel_ratio"] = round(out["c4_ret1_4x64_vs_1216"]["kernel_us"]
+                                                   / out["c4_reuse_4x64_vs_608"]["kernel_us"], 3)
+    torch.cuda.empty_cache()
+    return out
+
+
+# (name, jobs, tokens per sequence, block start, block length, retention, head_select, Hq, Hkv): the
+# state-1 (selection) steps: C4 head-sparse, C4 token-level, C2 at retention 1.0 (token level, the
+# SparseConfig default), Dream GQA shape at retention 0.5
+SELECT_SHAPES = (
+    ("c4_head_select_4x1280", 4, 1280, 1024, 64, 0.5, True, 32, 32),
+    ("c4_token_select_4x1280", 4, 1280, 1024, 64, 0.5, False, 32, 32),
+    ("c2_cached_8x384_ret1", 8, 384, 256, 32, 1.0, False, 32, 32),
+    ("dream_gqa_16x832", 16, 832, 576, 32, 0.5, True, 28, 4),
+)
+
+
+def bench_select(dev, n_layers=4):
+    """K5/K6 (selection + fused scatter of the kept rows into the paged
+    cache) per layer call, rotating n_layers layers' q/k/v and caches.
+    Bytes (algorithmic): read the block queries and the candidate keys for
+    scoring, read the kept K/V rows and write them into the cache, write the
+    int64 indices."""
+    from dllm_serve_amd import _capi
+    from dllm_serve_amd.sparse.state import keep_count
+
+    D = 128
+    out = {}
+    for name, B, n_tok, bs, bl, ratio, hs, Hq, Hkv in SELECT_SHAPES:
+        Kc = n_tok - bl
+        keep = keep_count(Kc, ratio)
+        slots, n_pages = _paged_slots([keep] * B, seed=2)
+        g = torch.Generator(device=dev).manual_seed(0)
+        n = B * n_tok
+        layers = []
+        for _ in range(n_layers):
+            q = torch.randn(n, Hq, D, generator=g, device=dev, dtype=torch.bfloat16)
+            k = torch.randn(n, Hkv, D, generator=g, device=dev, dtype=torch.bfloat16)
+            v = torch.randn(n, Hkv, D, generator=g, device=dev, dtype=torch.bfloat16)
+            kc = torch.zeros(n_pages * 256, Hkv, D, dtype=torch.bfloat16, device=dev)
+            layers.append((q, k, v, kc, torch.zeros_like(kc)))
+        jobs = torch.tensor([[b * n_tok, n_tok, bs, bl, keep, b * keep, int(hs), 3] for b in range(B)],
+                            dtype=torch.int32, device=dev)
+        sl = torch.tensor(slots, dtype=torch.int32, device=dev)
+        idx = torch.empty(B, Hkv, keep, dtype=torch.int64, device=dev)
+        ws = torch.empty(_capi.select_workspace_size(B, Kc, Hq, Hkv, D), dtype=torch.uint8, device=dev)
+        state = {"i": 0}
+
+        def one():
+            q, k, v, kc, vc = layers[state["i"] % n_layers]
+            state["i"] += 1
+            _capi.select_kv_store(q, k, v, jobs, B, Kc, keep, np.float32(D ** 0.5), kc, vc, sl, idx, ws)
+
+        reps = [time_kernel(one, iters=8 * n_layers, settle_s=0.05 if r else 0.1) for r in range(5)]
+        ms = sorted(reps)[2]
+        byts = B * (2.0 * (bl * Hq * D + Kc * Hkv * D) + 8.0 * keep * Hkv * D + 8.0 * Hkv * keep)
+        out[name] = dict(us=round(ms * 1e3, 2), kept_rows=keep, bytes_per_call=byts,
+                         gbs=round(byts / (ms * 1e-3) / 1e9, 1),
+                         frac_of_hbm=round(byts / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4))
+        del layers
+    torch.cuda.empty_cache()
+    return out
+
+
 def bench_sparse_c4(dev, steps_block=64, quick=False, n_layers=8):
     """C4 attention per 64-step block and per layer (B=4, P=1024, gen 256,
     block 64, LLaDA shape): sparse = head_select retention 0.5 (1 full step,
     1 full step + selection/store, 62 reuse steps); dense = 64 full recompute
-    steps.  Each step runs n_layers layers (own q/k/v and cache pages each)
-    back to back between two HIP events, as the model does, so the host work
-    of one call overlaps the kernels of the previous ones; the figure is the
-    step time divided by n_layers."""
+    steps.  Each step runs n_layers layers (own q/k/v and cache pages each);
+    the figure is the block's time divided by n_layers.
+
+    Primary figures: the steps as the device-step path runs them -- each
+    step's tables built on the device and the step replayed from a HIP graph
+    captured once per launch shape (StepGraphs).  Two blocks run; the second,
+    all replays enqueued back to back, is timed with HIP events around the
+    block.  `eager`: the
+    same block with every Attention.forward called from the host, timed from
+    before each step's host plan (StepPlan: tables built on the host and
+    copied over, shared by the step's layers) and from after it."""
+    from dllm_serve_amd.engine.device_step import DeviceStepState, StepGraphs
     from dllm_serve_amd.engine.sequence import PageAllocator, Sequence, prepare_step
     from dllm_serve_amd.layers.attention import Attention
     from dllm_serve_amd.sparse.state import SparseConfig
@@ -245,7 +387,7 @@ def bench_sparse_c4(dev, steps_block=64, quick=False, n_layers=8):
     D = 128
     B, P, gen, blk = 4, 1024, 256, 64
 
-    def run(cfg):
+    def run(cfg, graphed):
         attns = [Attention(Hq, D, D ** -0.5, Hkv, causal=False) for _ in range(n_layers)]
         pages = 4 * 8
         cache = torch.zeros(2, n_layers, pages, 256, Hkv, D, dtype=torch.bfloat16, device=dev)
@@ -262,29 +404,62 @@ def bench_sparse_c4(dev, steps_block=64, quick=False, n_layers=8):
                  torch.randn(B * (P + gen), Hkv, D, generator=g, device=dev, dtype=torch.bfloat16))
                 for _ in range(n_layers)]
         torch.cuda.synchronize()
-        total = 0.0
-        t = Timer()
+        total = total_plan = 0.0
+        t_all, t = Timer(), Timer()
+        if graphed:
+            def step_fn(tables):
+                n = tables.layout.total_rows
+                for a, (q, k, v) in zip(attns, full):
+                    a(q[:n], k[:n], v[:n])
+
+            tok = torch.zeros(B, P + gen, dtype=torch.int64, device=dev)
+            sg = StepGraphs(DeviceStepState(seqs, dev, tok.stride(0)), step_fn)
+            for block in range(2):
+                if block:  # the second block's replays, enqueued back to back
+                    torch.cuda.synchronize()
+                    t.start()
+                for step in range(steps_block):
+                    sg.run(seqs)
+                    for s in seqs:
+                        s.advance()
+                if block:
+                    total = t.stop_ms() / n_layers
+            del sg
+            torch.cuda.synchronize()
+            del full, cache
+            return total, None
         for step in range(steps_block):
             prepare_step(seqs, dev)
             rows = sum(s.step_rows()[1] for s in seqs)
-            attns[0]._plan(get_context(), dev)  # per-step host plan, shared by all layers: not timed
+            t_all.start()  # the GPU is idle here (the previous step ended with a synchronisation)
+            attns[0]._plan(get_context(), dev)  # per-step host plan, shared by all layers
             t.start()
             for a, (q, k, v) in zip(attns, full):
                 a(q[:rows], k[:rows], v[:rows])
             total += t.stop_ms() / n_layers
+            total_plan += t_all.a.elapsed_time(t.b) / n_layers
             reset_context()
             for s in seqs:
                 s.advance()
         del full, cache
-        return total
+        return total, total_plan
 
-    ms_sparse = run(SparseConfig(enabled=True, default_block_len=blk, retention_ratio=0.5, pool_kernel=3,
-                                 delay_step=1, head_select=True))
-    ms_cached_full = run(SparseConfig(enabled=True, default_block_len=blk, retention_ratio=1.0, pool_kernel=3,
-                                      delay_step=1, head_select=True))
-    ms_dense = run(None)
-    return dict(ms_per_block_sparse=ms_sparse, ms_per_block_ret1=ms_cached_full, ms_per_block_dense=ms_dense,
-                speedup_vs_dense=ms_dense / ms_sparse, speedup_vs_ret1=ms_cached_full / ms_sparse)
+    cfgs = dict(sparse=SparseConfig(enabled=True, default_block_len=blk, retention_ratio=0.5, pool_kernel=3,
+                                    delay_step=1, head_select=True),
+                ret1=SparseConfig(enabled=True, default_block_len=blk, retention_ratio=1.0, pool_kernel=3,
+                                  delay_step=1, head_select=True),
+                dense=None)
+    graphed = {k: run(c, True)[0] for k, c in cfgs.items()}
+    eager = {k: run(c, False) for k, c in cfgs.items()}
+    out = {f"ms_per_block_{k}": v for k, v in graphed.items()}
+    out.update(speedup_vs_dense=graphed["dense"] / graphed["sparse"], speedup_vs_ret1=graphed["ret1"] / graphed["sparse"])
+    ea = {f"ms_per_block_{k}": v[0] for k, v in eager.items()}
+    ea.update({f"ms_per_block_{k}_with_host_plan": v[1] for k, v in eager.items()})
+    ea.update(speedup_vs_dense=eager["dense"][0] / eager["sparse"][0],
+              speedup_vs_ret1=eager["ret1"][0] / eager["sparse"][0],
+              speedup_vs_ret1_with_host_plan=eager["ret1"][1] / eager["sparse"][1])
+    out["eager"] = ea
+    return out
 
 
 # ---------------------------------------------------------------------------
@@ -606,94 +781,143 @@ def bench_sampler(dev):
     return out
 
 
-def cpu_baseline(lens, Hq, Hkv, D, budget_s=12.0):
-    """Oracle (numpy fp32) attention of the headline step's layer calls on the
-    host cores; bounded sample of whole layer calls."""
+def cpu_setup():
+    """Host threads for the CPU oracle runs: every core in this process's
+    affinity set, capped by OMP_NUM_THREADS when the environment sets one (a
+    shared host's per-GPU share of cores); torch and the BLAS pool numpy uses
+    both get that count.  Returns (threads, affinity cores, CPU model)."""
+    cores = len(os.sched_getaffinity(0))
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    threads = min(cores, int(env)) if env.isdigit() and int(env) > 0 else cores
+    torch.set_num_threads(threads)
+    try:
+        from threadpoolctl import threadpool_limits
+        threadpool_limits(limits=threads)
+    except ImportError:
+        pass
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return threads, cores, model
+
+
+def cpu_timed(fn, reps=5):
+    """One untimed warm-up, then the median of `reps` perf_counter runs (s)."""
+    fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return sorted(ts)[len(ts) // 2]
+
+
+def cpu_baseline(lens, Hq, Hkv, D):
+    """Oracle (numpy fp32) attention of one headline layer call (8 x 384
+    tokens, 32 heads x 128) on the host cores: one warm-up, median of 5."""
     from oracle import attention as oatt
     from oracle.configs import attention_flops, packed_qkv
 
+    threads, cores, model = cpu_setup()
     q, k, v, cu = packed_qkv(lens, Hq, Hkv, D, seed=0, dtype=torch.float32)
     qn, kn, vn, cun = q.numpy(), k.numpy(), v.numpy(), cu.numpy()
-    oatt.varlen(qn[:cun[1]], kn[:cun[1]], vn[:cun[1]], cun[:2], cun[:2], D ** -0.5, dtype=np.float32)  # warm
-    t0 = time.perf_counter()
-    calls = 0
-    while True:
-        oatt.varlen(qn, kn, vn, cun, cun, D ** -0.5, dtype=np.float32)
-        calls += 1
-        if time.perf_counter() - t0 > budget_s or calls >= 64:
-            break
-    dt = time.perf_counter() - t0
-    flops = attention_flops(lens, lens, Hq, D) * calls
-    cores = len(os.sched_getaffinity(0))
-    return dict(value=flops / dt / 1e12, unit="TFLOP/s", cores=cores, kind="port",
-                sample=f"{calls} layer call(s) of the headline step (8 x 384 tokens, 32 heads x 128), "
-                       f"numpy fp32 oracle, {dt:.1f} s, threads = BLAS default on {cores} host cores")
+    t = cpu_timed(lambda: oatt.varlen(qn, kn, vn, cun, cun, D ** -0.5, dtype=np.float32))
+    flops = attention_flops(lens, lens, Hq, D)
+    return dict(value=flops / t / 1e12, unit="TFLOP/s", cores=threads, kind="port",
+                sample=f"one layer call of the headline step (8 x 384 tokens, 32 heads x 128), numpy fp32 oracle: "
+                       f"1 warm-up + median of 5 = {t:.3f} s; {threads} threads ({cores} cores in the affinity "
+                       f"set), {model}", cpu_model=model, seconds=t)
 
 
 def cpu_other_configs():
     """The oracle (numpy fp32) on the other configurations' single layer calls,
-    on the host cores: C1 whole attention (1 x 512 tokens), C4 full step
-    (4 x 1280) and reuse step (4 x 64 rows against 608 cached + 64 block rows),
-    C5 (32 x 32 rows against 2048-4096 cached rows)."""
+    on the host cores (one warm-up, median of 5 each): C1 whole attention
+    (1 x 512 tokens), C4 full step (4 x 1280), C4 selection + scatter (4 jobs
+    of 1280 tokens, head_select, 608 kept) and reuse step (4 x 64 rows
+    against 608 cached + 64 block rows), C5 (32 x 32 rows against 2048-4096
+    cached rows)."""
     from oracle import attention as oatt
     from oracle import configs
+    from oracle import select as osel
 
+    threads, cores, model = cpu_setup()
     out = {}
-
-    def timed(fn, reps):
-        fn()
-        ts = []
-        for _ in range(reps):
-            t0 = time.perf_counter()
-            fn()
-            ts.append(time.perf_counter() - t0)
-        return sorted(ts)[len(ts) // 2]
-
     q, k, v, cu, scale = configs.c1_single_layer()
     qn, kn, vn, cun = q.numpy(), k.numpy(), v.numpy(), cu.numpy()
-    t = timed(lambda: oatt.varlen(qn, kn, vn, cun, cun, scale, dtype=np.float32), 5)
+    t = cpu_timed(lambda: oatt.varlen(qn, kn, vn, cun, cun, scale, dtype=np.float32))
     fl = configs.attention_flops([512], [512], 32, 128)
     out["c1_512_tokens"] = dict(seconds=round(t, 4), gflops=round(fl / t / 1e9, 1))
     q, k, v, cu = configs.packed_qkv([1280] * 4, 32, 32, 128, seed=4, dtype=torch.float32)
     qn, kn, vn, cun = q.numpy(), k.numpy(), v.numpy(), cu.numpy()
-    t = timed(lambda: oatt.varlen(qn, kn, vn, cun, cun, 128 ** -0.5, dtype=np.float32), 1)
+    t = cpu_timed(lambda: oatt.varlen(qn, kn, vn, cun, cun, 128 ** -0.5, dtype=np.float32))
     fl = configs.attention_flops([1280] * 4, [1280] * 4, 32, 128)
     out["c4_full_step_layer"] = dict(seconds=round(t, 3), gflops=round(fl / t / 1e9, 1))
+    # C4 selection + scatter (state 1) of one layer: the oracle's head_select
+    # rule on bf16 inputs, then the kept rows written into a paged cache
+    qb, kb, vb, _ = configs.packed_qkv([1280] * 4, 32, 32, 128, seed=5)
+    qs, ks, vs = (x.float().numpy() for x in (qb, kb, vb))
+    n_keep, Kc = 608, 1216
+    kcache = np.zeros((4 * n_keep, 32, 128), dtype=np.float32)
+    vcache = np.zeros_like(kcache)
+
+    cand = np.concatenate([np.arange(1024), np.arange(1088, 1280)])  # prefix and suffix rows around the block
+
+    def select_store():
+        for i in range(4):
+            qi, ki, vi = qs[i * 1280:(i + 1) * 1280], ks[i * 1280:(i + 1) * 1280], vs[i * 1280:(i + 1) * 1280]
+            idx = osel.select(qi[1024:1088], ki[cand], n_keep, True, 3, np.float32(128 ** 0.5))
+            rows = cand[idx]  # [Hkv, n_keep] token rows per KV head
+            for h in range(32):
+                kcache[i * n_keep:(i + 1) * n_keep, h] = ki[rows[h], h]
+                vcache[i * n_keep:(i + 1) * n_keep, h] = vi[rows[h], h]
+
+    t = cpu_timed(select_store)
+    by = 4 * (2.0 * (64 * 32 * 128 + Kc * 32 * 128) + 8.0 * n_keep * 32 * 128 + 8.0 * 32 * n_keep)
+    out["c4_select_store_layer"] = dict(seconds=round(t, 3), gbs_bf16_equivalent=round(by / t / 1e9, 2))
     rng = np.random.default_rng(0)
     n_c, blk = 608, 64
     kc = rng.standard_normal((4 * n_c, 32, 128)).astype(np.float32)
     vc = rng.standard_normal((4 * n_c, 32, 128)).astype(np.float32)
-    qb = rng.standard_normal((4 * blk, 32, 128)).astype(np.float32)
+    qr = rng.standard_normal((4 * blk, 32, 128)).astype(np.float32)
     slots = [list(range(i * n_c, (i + 1) * n_c)) for i in range(4)]
 
     def reuse():
         for i in range(4):
             r = slice(i * blk, (i + 1) * blk)
-            oatt.block_cached(qb[r], qb[r], qb[r], kc, vc, slots[i], 128 ** -0.5, dtype=np.float32)
+            oatt.block_cached(qr[r], qr[r], qr[r], kc, vc, slots[i], 128 ** -0.5, dtype=np.float32)
 
-    t = timed(reuse, 3)
+    t = cpu_timed(reuse)
     fl = configs.attention_flops([blk] * 4, [n_c + blk] * 4, 32, 128)
     by = configs.attention_bytes([blk] * 4, [n_c + blk] * 4, 32, 32, 128)
     out["c4_reuse_step_layer"] = dict(seconds=round(t, 4), gflops=round(fl / t / 1e9, 1),
                                       gbs_bf16_equivalent=round(by / t / 1e9, 2))
     c = configs.c5_cached()
     kp, vp = c["k_pre"].float().numpy(), c["v_pre"].float().numpy()
-    qc, kb, vb = c["q"].float().numpy(), c["k"].float().numpy(), c["v"].float().numpy()
+    qc, kb5, vb5 = c["q"].float().numpy(), c["k"].float().numpy(), c["v"].float().numpy()
     off = np.cumsum([0] + c["prefix"])
     slots5 = [list(range(off[i], off[i + 1])) for i in range(len(c["prefix"]))]  # prefixes packed in order
 
     def c5():
         for i in range(len(c["prefix"])):
             r = slice(i * c["blk"], (i + 1) * c["blk"])
-            oatt.block_cached(qc[r], kb[r], vb[r], kp, vp, slots5[i], 128 ** -0.5, dtype=np.float32)
+            oatt.block_cached(qc[r], kb5[r], vb5[r], kp, vp, slots5[i], 128 ** -0.5, dtype=np.float32)
 
-    t = timed(c5, 1)
+    t = cpu_timed(c5)
     blks = [c["blk"]] * len(c["prefix"])
     fl = configs.attention_flops(blks, [p + c["blk"] for p in c["prefix"]], 32, 128)
     by = configs.attention_bytes(blks, [p + c["blk"] for p in c["prefix"]], 32, 32, 128)
     out["c5_layer"] = dict(seconds=round(t, 3), gflops=round(fl / t / 1e9, 1),
                            gbs_bf16_equivalent=round(by / t / 1e9, 2))
-    out["cores"] = len(os.sched_getaffinity(0))
+    out["threads"] = threads
+    out["cores_in_affinity_set"] = cores
+    out["cpu_model"] = model
+    out["timing"] = "1 warm-up + median of 5 perf_counter runs each"
     out["kind"] = "port"
     return out
 
@@ -800,12 +1024,13 @@ def main() -> None:
         c3 = c3_lens()
         r3 = bench_dense(c3, 28, 4, D, 4, 3, 1, dev, seed=3)
         extra["c3_dream_gqa_varlen"] = dict(lens=c3, kernel_us=round(r3["kernel_us"], 2),
-                                            tflops=round(r3["tflops_kernel"], 1))
+                                            tflops=round(r3["tflops_kernel"], 1),
+                                            mfma_frac=round(r3["tflops_kernel"] / PEAK_BF16_TFLOPS, 4))
         log("C4 full-step shape: 4 x 1280 tokens")
         r4 = bench_dense([1280] * 4, Hq, Hkv, D, 4, 3, 1, dev, seed=4)
         extra["c4_full_step_attention"] = dict(kernel_us=round(r4["kernel_us"], 2),
                                                tflops=round(r4["tflops_kernel"], 1),
-                                               frac_of_peak=round(r4["tflops_kernel"] / PEAK_BF16_TFLOPS, 4))
+                                               mfma_frac=round(r4["tflops_kernel"] / PEAK_BF16_TFLOPS, 4))
         log("C5: block-cached attention + KV scatter")
         r5 = bench_block_cached(dev, args.quick)
         extra["c5_block_cached"] = {k: round(v, 3) for k, v in r5.items()}
@@ -818,7 +1043,12 @@ def main() -> None:
                                for k, v in bench_sampler(dev).items()}
         log("C4: sparse vs dense attention per 64-step block")
         r4s = bench_sparse_c4(dev)
-        extra["c4_head_sparse_per_block"] = {k: round(v, 3) for k, v in r4s.items()}
+        extra["c4_head_sparse_per_block"] = {k: (round(v, 3) if not isinstance(v, dict) else
+                                                 {kk: round(vv, 3) for kk, vv in v.items()}) for k, v in r4s.items()}
+        log("K3b at the denoise-loop reuse shapes (8 layers' caches rotated)")
+        extra["block_cached_denoise_shapes"] = bench_denoise_shapes(dev)
+        log("K5/K6 selection + scatter at the state-1 shapes")
+        extra["select_store"] = bench_select(dev)
     if not args.quick:
         log("C2 full model: LLaDA-8B denoise, B=8, prompt 256, gen 128, 128 steps (cached and dense)")
         extra["c2_denoise_llada8b"] = bench_denoise(dev)
@@ -829,6 +1059,7 @@ def main() -> None:
         log("CPU baseline (oracle)")
         cpu = cpu_baseline(lens, Hq, Hkv, D)
         cpu["value"] = round(cpu["value"], 4)
+        cpu["seconds"] = round(cpu["seconds"], 4)
         log("CPU oracle on the other configurations' layer calls")
         extra["cpu_oracle_other_configs"] = cpu_other_configs()
     # The binding ceiling of the headline kernel: HBM when its arithmetic

@@ -967,6 +967,80 @@ def profile_run(lens, Hq, Hkv, D, n_layers, dev):
         f"({n} tokens), 1 C5 store + 4 C5 block-cached launches, 8 + 8 K8 launches (1024 and 256 x {V} logits)")
 
 
+def profile_denoise_run(dev):
+    """Fixed dispatch sequence for counter runs of the denoise-loop kernels:
+    three 256 MiB device copies (counter calibration); K3b at each
+    DENOISE_CACHED_SHAPES case, 16 launches rotating 8 layers' caches; the
+    selection chain at each SELECT_SHAPES case, 8 launches rotating 4
+    layers; the dense kernel at C3 (16 ragged Dream GQA segments) and at the
+    C4 full step (4 x 1280), 4 launches each over distinct layers."""
+    from oracle.configs import c3_lens
+    from dllm_serve_amd import _capi
+    from dllm_serve_amd.sparse.state import keep_count
+
+    D = 128
+    src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    for name, B, Lq, n_c, Hq, Hkv in DENOISE_CACHED_SHAPES:
+        slots, n_pages = _paged_slots([n_c] * B, seed=1)
+        g = torch.Generator(device=dev).manual_seed(0)
+        n = B * Lq
+        layers = [tuple(torch.randn(r, H, D, generator=g, device=dev, dtype=torch.bfloat16)
+                        for r, H in ((n, Hq), (n, Hkv), (n, Hkv), (n_pages * 256, Hkv), (n_pages * 256, Hkv)))
+                  for _ in range(8)]
+        o = torch.empty(n, Hq, D, dtype=torch.bfloat16, device=dev)
+        cu = torch.arange(0, n + 1, Lq, dtype=torch.int32, device=dev)
+        sl = torch.tensor(slots, dtype=torch.int32, device=dev)
+        so = torch.tensor([i * n_c for i in range(B + 1)], dtype=torch.int32, device=dev)
+        ws_b = _capi.block_cached_workspace_size(B, Lq, n_c + Lq, Hq, Hkv, D)
+        ws = torch.empty(max(ws_b, 16), dtype=torch.uint8, device=dev) if ws_b else None
+        for i in range(16):
+            q, k, v, kc, vc = layers[i % 8]
+            _capi.attn_block_cached_fwd(q, k, v, o, cu, None, B, Lq, n_c + Lq, kc, vc, sl, so, D ** -0.5, ws)
+        torch.cuda.synchronize()
+        del layers
+        log(f"profile: K3b {name}, 16 launches")
+    for name, B, n_tok, bs, bl, ratio, hs, Hq, Hkv in SELECT_SHAPES:
+        Kc = n_tok - bl
+        keep = keep_count(Kc, ratio)
+        slots, n_pages = _paged_slots([keep] * B, seed=2)
+        g = torch.Generator(device=dev).manual_seed(0)
+        n = B * n_tok
+        layers = [tuple(torch.randn(r, H, D, generator=g, device=dev, dtype=torch.bfloat16)
+                        for r, H in ((n, Hq), (n, Hkv), (n, Hkv))) for _ in range(4)]
+        kc = torch.zeros(n_pages * 256, Hkv, D, dtype=torch.bfloat16, device=dev)
+        vc = torch.zeros_like(kc)
+        jobs = torch.tensor([[b * n_tok, n_tok, bs, bl, keep, b * keep, int(hs), 3] for b in range(B)],
+                            dtype=torch.int32, device=dev)
+        sl = torch.tensor(slots, dtype=torch.int32, device=dev)
+        idx = torch.empty(B, Hkv, keep, dtype=torch.int64, device=dev)
+        ws = torch.empty(_capi.select_workspace_size(B, Kc, Hq, Hkv, D), dtype=torch.uint8, device=dev)
+        for i in range(8):
+            q, k, v = layers[i % 4]
+            _capi.select_kv_store(q, k, v, jobs, B, Kc, keep, np.float32(D ** 0.5), kc, vc, sl, idx, ws)
+        torch.cuda.synchronize()
+        del layers
+        log(f"profile: selection {name}, 8 launches")
+    for name, lens, Hq, Hkv in (("c3", c3_lens(), 28, 4), ("c4_full", [1280] * 4, 32, 32)):
+        layers = make_layers(lens, Hq, Hkv, D, 4, dev, seed=3)
+        order = sorted(range(len(lens)), key=lambda i: (-lens[i], i))  # the step plan's segment order
+        ids = torch.tensor(order, dtype=torch.int32, device=dev)
+        cu = torch.zeros(len(lens) + 1, dtype=torch.int32)
+        cu[1:] = torch.cumsum(torch.tensor(lens, dtype=torch.int32), 0)
+        cu = cu.to(dev)
+        for q, k, v in layers:
+            o = torch.empty_like(q)
+            _capi.attn_varlen_fwd(q, k, v, o, cu, cu, None if order == list(range(len(lens))) else ids,
+                                  len(lens), max(lens), D ** -0.5)
+        torch.cuda.synchronize()
+        del layers
+        log(f"profile: dense {name}, 4 launches")
+
+
 TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "attn_dense_kernel_llada_c2_8x384_counters.md")
 
 
@@ -991,11 +1065,13 @@ def main() -> None:
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--quick", action="store_true", help="headline only (no extra shapes, no CPU baseline)")
-    ap.add_argument("--profile", action="store_true",
-                    help="counter run: a 256 MiB device copy (x3, calibrates FETCH_SIZE / WRITE_SIZE), 32 "
-                         "launches of the headline attention kernel, 32 RoPE launches, the C5 store, 4 C5 "
-                         "block-cached launches and 8 softmax-max launches over 1024 x 126464 logits; "
-                         "prints no JSON")
+    ap.add_argument("--profile", nargs="?", const="headline", choices=("headline", "denoise"),
+                    help="counter run, prints no JSON.  headline: a 256 MiB device copy (x3, calibrates "
+                         "FETCH_SIZE / WRITE_SIZE), 32 launches of the headline attention kernel, 32 RoPE "
+                         "launches, the C5 store, 4 C5 block-cached launches and 8 softmax-max launches over "
+                         "1024 x 126464 logits.  denoise: the copies, then block-cached attention at the "
+                         "denoise reuse shapes, the selection chain at the state-1 shapes and the dense kernel "
+                         "at C3 and the C4 full step")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the library has no multi-GPU path",
@@ -1012,8 +1088,11 @@ def main() -> None:
     D = 128
     lens = [256 + 128] * 8
     n_layers = 32
-    if args.profile:
+    if args.profile == "headline":
         profile_run(lens, Hq, Hkv, D, n_layers, dev)
+        return
+    if args.profile == "denoise":
+        profile_denoise_run(dev)
         return
     log("headline: C2 dense step attention, 32 layers x 8 x 384 tokens")
     r = bench_dense(lens, Hq, Hkv, D, n_layers, args.steps, args.warmup, dev)

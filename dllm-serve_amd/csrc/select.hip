@@ -3,27 +3,28 @@
 // job (sequence) carries its own head_select and pool_kernel, so one launch
 // serves a step whose sequences use different SparseConfigs.
 //
-// Four launches per call:
-//   1. qbar_kernel   block mean of q per (job, query head): the block rows
-//                    are staged through LDS and summed in f64, rows in
-//                    order, one thread per two d.
-//   2. score_kernel  per (job, KV head, 256 candidates): the candidates' K
-//                    rows of that head are loaded coalesced into LDS, then
-//                    each lane computes its candidate's dot products with
-//                    the g query heads of the KV head (f64, d ascending):
-//                    head_select -> the bf16 maximum over the g heads;
-//                    token selection -> the f64 sum of the g dots.
-//   3. topk_kernel   per (job, selection head): pool + scale into 16-bit
-//                    order keys, a two-level byte histogram finds the
-//                    threshold key of the n_keep-th best candidate, an
-//                    index-order compaction takes every better candidate and
-//                    the first ties, and a sort orders the n_keep selected
-//                    rows (score descending, candidate index ascending):
-//                    bitonic over unique 64-bit keys in LDS, or for more than
+// Two launches per call:
+//   1. score_kernel  per (job, KV head, 256 candidates): the block mean of q
+//                    for the g query heads of the KV head (f64 sums, rows in
+//                    order; every workgroup of the KV head computes it from
+//                    the block rows, while its candidates' K rows are in
+//                    flight), the K rows staged coalesced through LDS, then
+//                    each lane's dot products with the g heads (f64, d
+//                    ascending): head_select -> the bf16 maximum over the g
+//                    heads; token selection -> the f64 sum of the g dots.
+//   2. topk_kernel   per (job, KV head): pool + scale into 16-bit order
+//                    keys, a two-level byte histogram finds the threshold key
+//                    of the n_keep-th best candidate, an index-order
+//                    compaction takes every better candidate and the first
+//                    ties, and a sort orders the n_keep selected rows (score
+//                    descending, candidate index ascending): in registers,
+//                    bitonic over unique keys in LDS, or for more than
 //                    kSortCap rows a stable two-pass radix sort in the
-//                    workspace.  No limit on the candidate count.
-//   4. sel_copy_kernel  copies every selected (rank, head) row piece, 16
-//                    bytes per thread, into its cache slot.
+//                    workspace.  No limit on the candidate count.  The
+//                    workgroup then copies its KV head's piece of every
+//                    selected row into the row's cache slot.  Token-selection
+//                    jobs make the same (shared) selection in every KV head's
+//                    workgroup.
 // The arithmetic follows a fixed, order-defined rule (f64 sums in a stated
 // order, explicit f32 / bf16 rounding points, ties to the lower candidate
 // index), so the selected indices are reproducible bit for bit on the CPU.
@@ -36,7 +37,7 @@ namespace dllm {
 constexpr int SHD = 128;           // the head dim these kernels handle
 constexpr int kJobCols = 8;        // row0, n_tok, blk_start, blk_len, n_keep, slot_off, head_select, pool_k
 constexpr int kScoreCands = 256;   // candidates per score workgroup
-constexpr int kQbarRows = 64;      // block rows staged per qbar round
+constexpr int kQbarStage = 32768;  // bytes of block rows staged per qbar chunk (inside the K-tile area)
 constexpr int kTopkThreads = 1024;
 constexpr int kSortCap = 8192;     // selected rows sorted in LDS as 64-bit keys
 constexpr int kMaxGroup = 64;      // query heads per KV head
@@ -57,8 +58,8 @@ struct SelArgs {
   const int32_t* slots;
   int64_t n_slots;
   int64_t* idx_out;  // [n_job][Hkv][max_keep] or null
+  int n_part;        // top-k workgroups per (job, KV head): each selects, then copies 1/n_part of the rows
   // workspace
-  uint16_t* qbar;    // [n_job][Hq][128] bf16 bits
   uint16_t* raw;     // [n_job][Hkv][max_kc] bf16 bits (head_select jobs)
   double* part;      // [n_job][Hkv][max_kc] per-KV-head sums (token-selection jobs)
   uint16_t* okey;    // [n_job][Hkv][max_kc] pooled order keys
@@ -125,55 +126,16 @@ __device__ int block_excount(bool flag, int* wave_tot, int* total) {
   return base + below;
 }
 
-// ---- 1. block mean of q ------------------------------------------------------
-// grid (n_job, ceil(Hq / 4)), block 256 = 4 query heads x 64 threads:
-// qbar[j][h][d] = bf16(f32(f64 sum_t q[bs+t][h][d] / bl)), t ascending.  The
-// block rows of the 4 heads go through LDS kQbarRows at a time (every load of
-// a round in flight together); thread (head, l) then sums d = 2l and 2l + 1
-// row by row (64 lanes read 64 consecutive words: no bank conflicts).
-constexpr int kQbarHeads = 4;
-__global__ __launch_bounds__(256) void qbar_kernel(SelArgs a) {
-  __shared__ uint32_t tile[kQbarRows * kQbarHeads * 64];  // [row][head][64 words]
-  const int jid = blockIdx.x;
-  const int h0 = blockIdx.y * kQbarHeads;
-  const Job jb = load_job(a, jid);
-  if (jb.n_keep <= 0) return;
-  const int tid = threadIdx.x;
-  const int hh = tid >> 6, l = tid & 63;
-  const uint16_t* q0 = a.q + ((int64_t)jb.row0 + jb.bs) * a.q_stride + (int64_t)h0 * SHD;
-  double s0 = 0.0, s1 = 0.0;
-  for (int t0 = 0; t0 < jb.bl; t0 += kQbarRows) {
-    const int n = min(kQbarRows, jb.bl - t0);
-    // load: 16-byte chunk ch of (row r, head hl): 64 chunks per row, 4 rows per pass
-    for (int i = tid; i < n * kQbarHeads * 16; i += blockDim.x) {
-      const int r = i / (kQbarHeads * 16), rem = i - r * (kQbarHeads * 16);
-      const int hl = rem >> 4, ch = rem & 15;
-      if (h0 + hl < a.Hq)
-        *reinterpret_cast<u32x4_t*>(tile + (r * kQbarHeads + hl) * 64 + ch * 4) =
-            ld128(q0 + (int64_t)(t0 + r) * a.q_stride + hl * SHD + ch * 8);
-    }
-    __syncthreads();
-    if (h0 + hh < a.Hq) {
-      for (int r = 0; r < n; ++r) {
-        const uint32_t w = tile[(r * kQbarHeads + hh) * 64 + l];
-        s0 += (double)bf16_val(w & 0xffffu);
-        s1 += (double)bf16_val(w >> 16);
-      }
-    }
-    __syncthreads();
-  }
-  if (h0 + hh < a.Hq) {
-    uint16_t* out = a.qbar + ((int64_t)jid * a.Hq + h0 + hh) * SHD + 2 * l;
-    out[0] = (uint16_t)f64_to_bf16_bits_2step(s0 / (double)jb.bl);
-    out[1] = (uint16_t)f64_to_bf16_bits_2step(s1 / (double)jb.bl);
-  }
-}
-
-// ---- 2. scores ---------------------------------------------------------------
+// ---- 1. scores ---------------------------------------------------------------
 // grid (ceil(max_kc / 256), Hkv, n_job), block 256, dynamic LDS = 64 KiB of K
 // rows + the g query heads' qbar as f32.  K rows: 16 lanes per 256-byte row,
 // stored with 16-byte chunk c at c ^ (row & 15) so that the per-lane row reads
 // afterwards (lane = row) spread over all banks.
+// qbar[h][d] = bf16(f32(f64 sum_t q[bs+t][h][d] / bl)), t ascending: the
+// block rows of up to four query heads at a time go through LDS (the K-tile
+// area, before the K rows are stored there) in chunks of 32 KiB, loaded
+// while the K rows are in flight; thread (head slot tid / 64, pair l =
+// tid % 64) then sums d = 2l and 2l + 1 row by row.
 // dot(h, j) = sum_d qbar[h][d] * k[j][kv][d] in f64, d ascending (each product
 // of two bf16 values is exact in f64, so fma gives the same sums).
 __global__ __launch_bounds__(256) void score_kernel(SelArgs a) {
@@ -195,8 +157,61 @@ __global__ __launch_bounds__(256) void score_kernel(SelArgs a) {
     const int64_t row = (int64_t)jb.row0 + cand_row(jb, min(c, jb.kc - 1));
     rows[p] = ld128(a.k + row * a.k_stride + (int64_t)kv * SHD + ch * 8);
   }
-  const uint16_t* qb = a.qbar + ((int64_t)jid * a.Hq + (int64_t)kv * g) * SHD;
-  for (int i = tid; i < g * SHD; i += blockDim.x) qs[i] = bf16_val(qb[i]);
+  {
+    uint32_t* stage = reinterpret_cast<uint32_t*>(kt);  // [row][head of the pass][64 words]
+    const int hs = tid >> 6, l = tid & 63;
+    const uint16_t* qblk = a.q + ((int64_t)jb.row0 + jb.bs) * a.q_stride + (int64_t)kv * g * SHD;
+    for (int h0 = 0; h0 < g; h0 += 4) {
+      const int hp = min(4, g - h0);             // heads of this pass
+      const int rows_per = kQbarStage / (hp * 256);  // block rows per chunk
+      double s0 = 0.0, s1 = 0.0;
+      for (int t0 = 0; t0 < jb.bl; t0 += rows_per) {
+        const int n = min(rows_per, jb.bl - t0);
+        const int items = n * hp * 16;  // 16-byte pieces of the chunk
+        u32x4_t qv[kQbarStage / (256 * 16)];
+#pragma unroll
+        for (int u = 0; u < kQbarStage / (256 * 16); ++u) {
+          const int i = u * 256 + tid;
+          if (i < items) {
+            const int r = i / (hp * 16), rem = i - r * (hp * 16);
+            qv[u] = ld128(qblk + (int64_t)(t0 + r) * a.q_stride + (h0 + (rem >> 4)) * SHD + (rem & 15) * 8);
+          }
+        }
+        __syncthreads();  // the previous chunk is summed (and the first: nothing reads the area yet)
+#pragma unroll
+        for (int u = 0; u < kQbarStage / (256 * 16); ++u) {
+          const int i = u * 256 + tid;
+          if (i < items) *reinterpret_cast<u32x4_t*>(stage + i * 4) = qv[u];
+        }
+        __syncthreads();
+        if (hs < hp) {
+          // 16 rows' words read together, then added in row order
+          const uint32_t* sp = stage + hs * 64 + l;
+          int r = 0;
+          for (; r + 16 <= n; r += 16) {
+            uint32_t w[16];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) w[u] = sp[(r + u) * hp * 64];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+              s0 += (double)bf16_val(w[u] & 0xffffu);
+              s1 += (double)bf16_val(w[u] >> 16);
+            }
+          }
+          for (; r < n; ++r) {
+            const uint32_t w = sp[r * hp * 64];
+            s0 += (double)bf16_val(w & 0xffffu);
+            s1 += (double)bf16_val(w >> 16);
+          }
+        }
+      }
+      if (hs < hp) {
+        qs[(h0 + hs) * SHD + 2 * l] = bf16_val(f64_to_bf16_bits_2step(s0 / (double)jb.bl));
+        qs[(h0 + hs) * SHD + 2 * l + 1] = bf16_val(f64_to_bf16_bits_2step(s1 / (double)jb.bl));
+      }
+    }
+    __syncthreads();  // the stage area becomes the K tile
+  }
 #pragma unroll
   for (int p = 0; p < kScoreCands / 16; ++p) {
     const int r = 16 * p + rsub;
@@ -233,7 +248,7 @@ __global__ __launch_bounds__(256) void score_kernel(SelArgs a) {
     a.part[out] = part;
 }
 
-// ---- 3. top-k ------------------------------------------------------------------
+// ---- 2. top-k and copy ------------------------------------------------------------------
 // Bitonic sort, descending, of n (a power of two) unique 64-bit keys in LDS.
 __device__ void bitonic_desc_u64(uint64_t* keys, int n) {
   for (int kk = 2; kk <= n; kk <<= 1) {
@@ -401,29 +416,82 @@ __device__ __forceinline__ uint16_t raw_bits(const SelArgs& a, const Job& jb, in
   if (jb.head_select) return a.raw[((int64_t)jid * a.Hkv + h) * a.max_kc + u];
   double t = 0.0;
   const double* p = a.part + (int64_t)jid * a.Hkv * a.max_kc + u;
-  for (int kv = 0; kv < a.Hkv; ++kv) t += p[(int64_t)kv * a.max_kc];
+  int kv = 0;
+  for (; kv + 16 <= a.Hkv; kv += 16) {  // 16 loads in flight, added in head order
+    double x[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) x[i] = p[(int64_t)(kv + i) * a.max_kc];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) t += x[i];
+  }
+  for (; kv < a.Hkv; ++kv) t += p[(int64_t)kv * a.max_kc];
   return (uint16_t)f64_to_bf16_bits_2step(t);
 }
 
-// grid (Hkv, n_job), block 1024.  Token-selection jobs use selection head 0 only.
+// The copy of the selected rows of ranks [r0, r1) -- their KV-head-h pieces
+// -- into their cache slots by the whole workgroup: item i = (rank r0 + i / 16,
+// 16-byte chunk i % 16), eight items per thread in flight.  cand(r) gives the
+// candidate of rank r.
+template <typename CandFn>
+__device__ __forceinline__ void copy_selected(const SelArgs& a, const Job& jb, int h, int r0, int r1, CandFn cand) {
+  const int64_t row_elems = (int64_t)a.Hkv * SHD;
+  const int n_items = (r1 - r0) * 16;
+  constexpr int kPer = 8;
+  for (int i0 = 0; i0 < n_items; i0 += kPer * kTopkThreads) {
+    u32x4_t kx[kPer], vx[kPer];
+    int64_t dst[kPer];
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const int i = i0 + u * kTopkThreads + (int)threadIdx.x;
+      dst[u] = -1;
+      if (i < n_items) {
+        const int r = r0 + (i >> 4), chk = i & 15;
+        const int j = cand(r);
+        const int64_t slot = a.slots[jb.slot_off + r];
+        if (slot >= 0 && slot < a.cache_slots && j >= 0 && j < jb.kc) {
+          const int64_t row = (int64_t)jb.row0 + cand_row(jb, j);
+          const int64_t e = (int64_t)h * SHD + chk * 8;
+          kx[u] = ld128_stream(a.k + row * a.k_stride + e);
+          vx[u] = ld128_stream(a.v + row * a.v_stride + e);
+          dst[u] = slot * row_elems + e;
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kPer; ++u)
+      if (dst[u] >= 0) {
+        st128(a.k_cache + dst[u], kx[u]);
+        st128(a.v_cache + dst[u], vx[u]);
+      }
+  }
+}
+
+// grid (Hkv, n_job, n_part), block 1024.  Each of the n_part workgroups of
+// (job, KV head) makes the selection and copies one contiguous share of the
+// ranks (part 0 writes idx_out); token-selection jobs: every KV head's
+// workgroups make the same selection (from the summed partial dots) and
+// copy their own head's pieces, and only head 0 writes idx_out.  Beyond
+// kLdsCand candidates (the sort then goes through the workspace, one buffer
+// per (job, head)) part 0 alone selects and copies every rank.
 // LDS: 128 KiB pool (small path: raw bits, order keys and 32-bit sort keys of
-// up to kLdsCand candidates; large path: kSortCap 64-bit sort keys) + the
-// shared scratch.
+// up to kLdsCand candidates, then the selected candidates in rank order;
+// large path: kSortCap 64-bit sort keys) + the shared scratch.
 __global__ __launch_bounds__(kTopkThreads) void topk_kernel(SelArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t pool[128 * 1024];
   __shared__ TopkShared sh;
   const int h = blockIdx.x;
   const int jid = blockIdx.y;
+  const int part = blockIdx.z;
   const Job jb = load_job(a, jid);
-  if (!jb.head_select && h > 0) return;
   const int kc = jb.kc, nk = jb.n_keep;
   if (kc <= 0 || nk <= 0) return;
+  if (part > 0 && kc > kLdsCand) return;
   const int tid = threadIdx.x;
   const int64_t base = ((int64_t)jid * a.Hkv + h) * a.max_kc;
   const int64_t sbase = ((int64_t)jid * a.Hkv + h) * a.max_keep;
   const int pk = jb.pool_k;
   const int pad = pk / 2;
-  int64_t* io = a.idx_out ? a.idx_out + sbase : nullptr;
+  int64_t* io = a.idx_out && part == 0 && (jb.head_select || h == 0) ? a.idx_out + sbase : nullptr;
   int32_t* so = a.sel + sbase;
   for (int b = tid; b < 256; b += blockDim.x) sh.hist[b] = 0;
 
@@ -480,12 +548,13 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(SelArgs a) {
     int P2 = 1;
     while (P2 < nk) P2 <<= 1;
     __syncthreads();
+    int32_t* selc = reinterpret_cast<int32_t*>(pool);  // rank -> candidate (raw bits / keys are dead)
     if (P2 <= kRegSort) {
       uint32_t x = tid < nk ? skey[tid] : 0u;  // 0 sorts below every real key
       x = bitonic_desc_reg(x, P2, sh.chunk);
       if (tid < nk) {
         const int c = 0xffff - (int)(x & 0xffffu);
-        so[tid] = c;
+        selc[tid] = c;
         if (io) io[tid] = c;
       }
     } else {
@@ -507,12 +576,16 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(SelArgs a) {
           __syncthreads();
         }
       }
+      // selc overlaps only the raw bits / order keys, skey lies behind them
       for (int r = tid; r < nk; r += blockDim.x) {
         const int c = 0xffff - (int)(skey[r] & 0xffffu);
-        so[r] = c;
+        selc[r] = c;
         if (io) io[r] = c;
       }
     }
+    __syncthreads();
+    const int r0 = (int)((int64_t)nk * part / a.n_part), r1 = (int)((int64_t)nk * (part + 1) / a.n_part);
+    copy_selected(a, jb, h, r0, r1, [&](int r) { return selc[r]; });
     return;
   }
 
@@ -588,41 +661,19 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(SelArgs a) {
     radix_pass(sh, a.ckey0 + sbase, a.cidx0 + sbase, a.ckey1 + sbase, a.cidx1 + sbase, nk, 0, nullptr);
     radix_pass(sh, a.ckey1 + sbase, a.cidx1 + sbase, nullptr, so, nk, 8, io);
   }
-}
-
-// ---- 4. copy of the selected rows into their cache slots -------------------
-// grid (ceil(max_keep * Hkv * 16 / 256), n_job), block 256: thread = one 16-byte
-// chunk of one (rank r, KV head) piece; head_select jobs take each head's row
-// from its own selection, token-selection jobs the same row for every head.
-__global__ __launch_bounds__(256) void sel_copy_kernel(SelArgs a) {
-  const int jid = blockIdx.y;
-  const Job jb = load_job(a, jid);
-  const int64_t x = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t piece = x >> 4;
-  const int ch = (int)(x & 15);
-  const int r = (int)(piece / a.Hkv);
-  const int h = (int)(piece - (int64_t)r * a.Hkv);
-  if (r >= jb.n_keep) return;
-  const int j = a.sel[((int64_t)jid * a.Hkv + (jb.head_select ? h : 0)) * a.max_keep + r];
-  const int64_t slot = a.slots[jb.slot_off + r];
-  if (slot < 0 || slot >= a.cache_slots || j < 0 || j >= jb.kc) return;
-  const int64_t row = (int64_t)jb.row0 + cand_row(jb, j);
-  const int64_t e = (int64_t)h * SHD + ch * 8;
-  const int64_t row_elems = (int64_t)a.Hkv * SHD;
-  st128(a.k_cache + slot * row_elems + e, ld128_stream(a.k + row * a.k_stride + e));
-  st128(a.v_cache + slot * row_elems + e, ld128_stream(a.v + row * a.v_stride + e));
+  __syncthreads();  // the workgroup's writes of so are visible to it
+  copy_selected(a, jb, h, 0, nk, [&](int r) { return so[r]; });
 }
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct SelLayout {
-  size_t qbar, raw, part, okey, sel, ckey, cidx, total;
+  size_t raw, part, okey, sel, ckey, cidx, total;
 };
 
 static SelLayout sel_layout(int n_job, int max_kc, int Hq, int Hkv) {
   SelLayout L;
   const size_t nj = (size_t)n_job, kc = (size_t)max_kc, hk = (size_t)Hkv;
-  L.qbar = align256(nj * Hq * SHD * 2);
   L.raw = align256(nj * hk * kc * 2);
   L.part = align256(nj * hk * kc * 8);
   L.okey = align256(nj * hk * kc * 2);
@@ -630,7 +681,7 @@ static SelLayout sel_layout(int n_job, int max_kc, int Hq, int Hkv) {
   const bool large = max_kc > kSortCap;
   L.ckey = large ? align256(nj * hk * kc * 2) : 0;
   L.cidx = large ? align256(nj * hk * kc * 4) : 0;
-  L.total = L.qbar + L.raw + L.part + L.okey + L.sel + 2 * L.ckey + 2 * L.cidx;
+  L.total = L.raw + L.part + L.okey + L.sel + 2 * L.ckey + 2 * L.cidx;
   return L;
 }
 
@@ -660,8 +711,9 @@ extern "C" int dllm_select_kv_store(const dllm_bf16* q, const dllm_bf16* k, cons
     return fail(DLLM_ERR_INVALID_ARG, "%s: negative size", name);
   if (n_job == 0 || max_kc == 0 || max_keep == 0) return DLLM_OK;
   if (max_keep > max_kc) return fail(DLLM_ERR_INVALID_ARG, "%s: max_keep %d > max_kc %d", name, max_keep, max_kc);
-  if ((int64_t)max_keep * Hkv * 16 / 256 + 1 >= ((int64_t)1 << 31) || (int64_t)max_kc / kScoreCands + 1 >= 65536 * 32)
-    return fail(DLLM_ERR_UNSUPPORTED, "%s: %d candidates / %d kept rows exceed the grid", name, max_kc, max_keep);
+  if ((int64_t)max_kc / kScoreCands + 1 >= ((int64_t)1 << 31) || n_job > 65535 || Hkv > 65535)
+    return fail(DLLM_ERR_UNSUPPORTED, "%s: %d jobs / %d candidates / %d KV heads exceed the grid", name, n_job, max_kc,
+                Hkv);
   if (!q || !k || !v || !jobs || !k_cache || !v_cache || !slots)
     return fail(DLLM_ERR_INVALID_ARG, "%s: null pointer", name);
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(k_cache) || !aligned16(v_cache) ||
@@ -685,7 +737,6 @@ extern "C" int dllm_select_kv_store(const dllm_bf16* q, const dllm_bf16* k, cons
   a.slots = slots; a.n_slots = n_slots; a.idx_out = idx_out;
   char* ws = reinterpret_cast<char*>(workspace);
   size_t o = 0;
-  a.qbar = reinterpret_cast<uint16_t*>(ws + o); o += L.qbar;
   a.raw = reinterpret_cast<uint16_t*>(ws + o); o += L.raw;
   a.part = reinterpret_cast<double*>(ws + o); o += L.part;
   a.okey = reinterpret_cast<uint16_t*>(ws + o); o += L.okey;
@@ -697,18 +748,16 @@ extern "C" int dllm_select_kv_store(const dllm_bf16* q, const dllm_bf16* k, cons
     a.cidx1 = reinterpret_cast<int32_t*>(ws + o); o += L.cidx;
   }
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  qbar_kernel<<<dim3(n_job, (Hq + kQbarHeads - 1) / kQbarHeads), dim3(256), 0, st>>>(a);
-  int rc = check_launch(name);
-  if (rc) return rc;
   const size_t score_lds = (size_t)kScoreCands * 256 + (size_t)a.g * SHD * sizeof(float);
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(score_kernel),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)score_lds);
   if (e != hipSuccess) return fail(DLLM_ERR_HIP, "%s: hipFuncSetAttribute: %s", name, hipGetErrorString(e));
   score_kernel<<<dim3((max_kc + kScoreCands - 1) / kScoreCands, Hkv, n_job), dim3(256), score_lds, st>>>(a);
-  if ((rc = check_launch(name))) return rc;
-  topk_kernel<<<dim3(Hkv, n_job), dim3(kTopkThreads), 0, st>>>(a);
-  if ((rc = check_launch(name))) return rc;
-  const int64_t pieces = (int64_t)max_keep * Hkv * 16;
-  sel_copy_kernel<<<dim3((unsigned)((pieces + 255) / 256), n_job), dim3(256), 0, st>>>(a);
+  int rc = check_launch(name);
+  if (rc) return rc;
+  // enough top-k workgroups to give every CU one (256 CUs), at most four per (job, KV head)
+  const int64_t pairs = (int64_t)n_job * Hkv;
+  a.n_part = (int)max((int64_t)1, min((int64_t)4, 256 / pairs));
+  topk_kernel<<<dim3(Hkv, n_job, a.n_part), dim3(kTopkThreads), 0, st>>>(a);
   return check_launch(name);
 }

@@ -38,8 +38,8 @@ def test_workspace_size_functions():
     assert _capi.block_cached_workspace_size(1024, 32, 4000, 32, 32, 128) == 0
     ws = _capi.block_cached_workspace_size(2, 32, 4128, 32, 32, 128)
     assert ws > 0 and ws % 4 == 0
-    # qbar, raw scores, token-selection partial sums, order keys, selections
-    assert _capi.select_workspace_size(4, 1216, 32, 32, 128) >= 4 * 32 * 128 * 2 + 4 * 32 * 1216 * (2 + 8 + 2 + 4)
+    # raw scores, token-selection partial sums, order keys, selections
+    assert _capi.select_workspace_size(4, 1216, 32, 32, 128) >= 4 * 32 * 1216 * (2 + 8 + 2 + 4)
     assert _capi.select_workspace_size(0, 10, 32, 32, 128) == 0
     # beyond the in-LDS sort the radix-sort ping-pong buffers are added
     small = _capi.select_workspace_size(1, 8192, 32, 32, 128)

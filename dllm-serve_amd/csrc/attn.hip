@@ -943,10 +943,13 @@ __global__ __launch_bounds__(256 * RB) __attribute__((amdgpu_waves_per_eu(2, 2))
 }
 
 // Merge the n_split partial records of every (segment, head, M row).
-// grid: (n_seg*Hkv*mtiles*32) rows / 2 per block; block 256 = 2 rows x 128 d.
+// grid: (n_seg*Hkv*mtiles*32) rows / 8 per block; block 256 = 8 rows x 32
+// threads, 4 d each (16-byte partial reads, 8-byte bf16 writes).  The split
+// loops are unrolled so that their loads are in flight together: one round
+// trip for the row maxima, one for the sums and accumulators.
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
-  const int row_rec = blockIdx.x * 2 + (threadIdx.x >> 7);  // (s, hkv, mt, q) flattened
-  const int d = threadIdx.x & 127;
+  const int row_rec = blockIdx.x * 8 + (threadIdx.x >> 5);  // (s, hkv, mt, q) flattened
+  const int d0 = (threadIdx.x & 31) * 4;
   const int total_rows = a.n_seg * a.Hkv * a.mtiles * 32;
   if (row_rec >= total_rows) return;
   const int q = row_rec & 31;
@@ -965,19 +968,27 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
   const int64_t P0 = (((int64_t)s * a.Hkv + hkv) * a.mtiles + mt) * a.n_split;
   const float* ml = a.ws + nrec * 32 * HD;
   float mx = -INFINITY;
+#pragma unroll 8
   for (int sp = 0; sp < a.n_split; ++sp) mx = fmaxf(mx, ml[((P0 + sp) * 32 + q) * 2]);
   const float mu = (mx == -INFINITY) ? 0.f : mx;
-  float l = 0.f, acc = 0.f;
+  float l = 0.f, acc0 = 0.f, acc1 = 0.f, acc2 = 0.f, acc3 = 0.f;
+#pragma unroll 8
   for (int sp = 0; sp < a.n_split; ++sp) {
     const float* rec = ml + ((P0 + sp) * 32 + q) * 2;
+    const f32x4_t x = *reinterpret_cast<const f32x4_t*>(a.ws + ((P0 + sp) * 32 + q) * HD + d0);
     const float w = (rec[0] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(rec[0] - mu);
     l += rec[1] * w;
-    acc += a.ws[((P0 + sp) * 32 + q) * HD + d] * w;
+    acc0 += x[0] * w;
+    acc1 += x[1] * w;
+    acc2 += x[2] * w;
+    acc3 += x[3] * w;
   }
   const float inv = l > 0.f ? 1.f / l : 0.f;
   const int tq = mrow / g;
   const int hq = hkv * g + (mrow - tq * g);
-  a.o[(int64_t)(qrow0 + tq) * a.o_stride + hq * HD + d] = (uint16_t)f32_to_bf16_bits(acc * inv);
+  uint32_t* op = reinterpret_cast<uint32_t*>(a.o + (int64_t)(qrow0 + tq) * a.o_stride + hq * HD + d0);
+  op[0] = cvt_pk_bf16(acc0 * inv, acc1 * inv);
+  op[1] = cvt_pk_bf16(acc2 * inv, acc3 * inv);
 }
 
 static const float kLog2e = 1.4426950408889634f;
@@ -1196,7 +1207,7 @@ static int block_cached_impl(const char* name, const dllm_bf16* q, const dllm_bf
   if ((rc = check_launch(name))) return rc;
   if (n_split > 1) {
     const int64_t rows = (int64_t)n_seg * Hkv * a.mtiles * 32;
-    attn_combine_kernel<<<dim3((unsigned)((rows + 1) / 2)), dim3(256), 0, st>>>(a);
+    attn_combine_kernel<<<dim3((unsigned)((rows + 7) / 8)), dim3(256), 0, st>>>(a);
     if ((rc = check_launch(name))) return rc;
   }
   return DLLM_OK;

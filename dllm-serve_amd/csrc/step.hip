@@ -58,28 +58,41 @@ __device__ __forceinline__ int keep_count(int kc, double ratio) {
   return (int)(k < kc ? k : kc);
 }
 
-// Exclusive prefix sum over the workgroup (one value per thread); returns the
-// thread's prefix and stores the total in *total.
-__device__ int block_exscan(int v, int* lds, int* total) {
+// Exclusive prefix sums of N values per thread over the workgroup, all N
+// scanned together (two barriers in all): ex[n] receives the thread's prefix
+// of value n and tot[n] the workgroup's total.  lds holds 16 * N ints.
+template <int N>
+__device__ void block_exscan_n(const int (&v)[N], int (&ex)[N], int (&tot)[N], int* lds) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  int x = v;
+  int x[N];
+#pragma unroll
+  for (int n = 0; n < N; ++n) x[n] = v[n];
 #pragma unroll
   for (int off = 1; off < 64; off <<= 1) {
-    const int y = __shfl_up(x, off);
-    if (lane >= off) x += y;
+#pragma unroll
+    for (int n = 0; n < N; ++n) {
+      const int y = __shfl_up(x[n], off);
+      if (lane >= off) x[n] += y;
+    }
   }
+  if (lane == 63)
+#pragma unroll
+    for (int n = 0; n < N; ++n) lds[wave * N + n] = x[n];
   __syncthreads();
-  if (lane == 63) lds[wave] = x;
-  __syncthreads();
-  int base = 0, all = 0;
-  for (int w = 0; w < (int)(blockDim.x >> 6); ++w) {
-    const int s = lds[w];
-    if (w < wave) base += s;
-    all += s;
+  const int nw = (int)(blockDim.x >> 6);
+#pragma unroll
+  for (int n = 0; n < N; ++n) {
+    int base = 0, all = 0;
+    for (int w = 0; w < nw; ++w) {
+      const int s = lds[w * N + n];
+      if (w < wave) base += s;
+      all += s;
+    }
+    ex[n] = base + x[n] - v[n];
+    tot[n] = all;
   }
-  *total = all;
-  return base + x - v;
+  __syncthreads();  // lds may be reused
 }
 
 __global__ __launch_bounds__(1024) void step_build_kernel(StepBuildArgs a) {
@@ -87,7 +100,7 @@ __global__ __launch_bounds__(1024) void step_build_kernel(StepBuildArgs a) {
   __shared__ int s_keep[kStepMaxSeq], s_sbase[kStepMaxSeq], s_pages[kStepMaxSeq];
   __shared__ int s_wlo[kStepMaxSeq], s_wn[kStepMaxSeq], s_woff[kStepMaxSeq];
   __shared__ int s_dense_rows[kStepMaxSeq];  // rows of a full-attention sequence, -1 otherwise
-  __shared__ int s_scan[16];
+  __shared__ int s_scan[16 * 8];
   const int i = threadIdx.x;
   const bool live = i < a.n;
   int mode = -1, rows = 0, start = 0, bs = 0, bl = 0, keep = 0, wlo = 0, wn = 0, sr = 0, first = 0, err = 0;
@@ -142,15 +155,13 @@ __global__ __launch_bounds__(1024) void step_build_kernel(StepBuildArgs a) {
     }
     if (sr == 0) err = err ? err : 4;
   }
-  int tot_rows, n_dense, n_cached, n_job, tot_cached_keep, tot_job_keep, tot_win, any_err;
-  const int cu0 = block_exscan(rows, s_scan, &tot_rows);
-  block_exscan(live && (mode == 0 || mode == 1), s_scan, &n_dense);
-  const int c_at = block_exscan(live && mode == 2, s_scan, &n_cached);
-  const int j_at = block_exscan(live && mode == 1, s_scan, &n_job);
-  const int ck = block_exscan(mode == 2 ? keep : 0, s_scan, &tot_cached_keep);
-  const int jk = block_exscan(mode == 1 ? keep : 0, s_scan, &tot_job_keep);
-  const int woff = block_exscan(wn, s_scan, &tot_win);
-  block_exscan(err != 0, s_scan, &any_err);
+  const int vals[8] = {rows, live && (mode == 0 || mode == 1), live && mode == 2, live && mode == 1,
+                       mode == 2 ? keep : 0, mode == 1 ? keep : 0, wn, err != 0};
+  int ex[8], tot[8];
+  block_exscan_n<8>(vals, ex, tot, s_scan);
+  const int cu0 = ex[0], c_at = ex[2], j_at = ex[3], ck = ex[4], jk = ex[5], woff = ex[6];
+  const int tot_rows = tot[0], n_dense = tot[1], n_cached = tot[2], n_job = tot[3];
+  const int tot_cached_keep = tot[4], tot_job_keep = tot[5], tot_win = tot[6], any_err = tot[7];
   // state-2 sequences' slots first, then state-1 sequences'
   const int sbase = mode == 2 ? ck : tot_cached_keep + jk;
   const int tot_slots = tot_cached_keep + tot_job_keep;

@@ -10,7 +10,10 @@ at full size against the oracle, and a step mixing SparseConfigs.
   cached rows.  Outputs within max-abs 2e-2 / mean-abs 2e-3 of the fp32 oracle
   (oracle.attention.mixed_step), the whole cache bit-exact after every step.
 - One step whose state-1 sequences use head_select True / False and pool
-  1 / 3 / 5, next to a dense sequence, through Attention.forward."""
+  1 / 3 / 5, next to a dense sequence, through Attention.forward.
+- A Dream-shaped batch (28 query / 4 KV heads, 16 ragged sequences, block
+  32): its reuse step runs the paired-row-block launch, once with every
+  sequence cached (no id table) and once next to a dense sequence."""
 import numpy as np
 import pytest
 import torch
@@ -133,3 +136,37 @@ def test_step_mixing_sparse_configs_through_the_layer(dev):
         return [dict(mode=2, rows=32)] * 3 + [dict(mode=0, rows=154)], slots
 
     _run_steps(dev, seqs, attn, cache, 3, descs, seed=77)
+
+
+@pytest.mark.parametrize("with_dense", [False, True])
+def test_dream_batch_paired_row_blocks_through_the_layer(dev, with_dense):
+    print(f"Dream batch: 16 ragged sequences, 28/4 heads, block 32, dense neighbour {with_dense}", flush=True)
+    Hq, Hkv = 28, 4
+    attn = Attention(Hq, D, D ** -0.5, Hkv, causal=False)
+    cfg = SparseConfig(enabled=True, default_block_len=32, retention_ratio=0.5, pool_kernel=3, delay_step=1,
+                       head_select=True)
+    prompts = [200 + (i * 53) % 300 for i in range(16)]
+    seqs = [Sequence([i + 1] * p, 64, MASK, cfg, device=dev) for i, p in enumerate(prompts)]
+    if with_dense:
+        seqs.append(Sequence([99] * 120, 32, MASK, None, device=dev))
+    n_pages = sum(s.num_blocks for s in seqs[:16]) + 1
+    alloc = PageAllocator(torch.randperm(n_pages, generator=torch.Generator().manual_seed(5)).tolist())
+    for s in seqs[:16]:
+        alloc.allocate(s)
+    cache = torch.zeros(2, n_pages, 256, Hkv, D, dtype=torch.bfloat16, device=dev)
+    attn.k_cache, attn.v_cache = cache[0], cache[1]
+    N = [p + 64 for p in prompts]
+    # 16 x 4 KV heads x 7 M tiles: more than one generation of single-block workgroups
+    assert 16 * Hkv * (32 * (Hq // Hkv) // 32) > 256
+    dense = [dict(mode=0, rows=152)] if with_dense else []
+
+    def descs(step):
+        if step == 0:
+            return [dict(mode=0, rows=n) for n in N] + dense, [[]] * len(seqs)
+        slots = [slot_mapping_for(s) for s in seqs[:16]] + ([[]] if with_dense else [])
+        if step == 1:
+            return [dict(mode=1, rows=n, blk_start=p, blk_len=32, n_keep=keep_count(n - 32, 0.5), head_select=True,
+                         pool_k=3) for n, p in zip(N, prompts)] + dense, slots
+        return [dict(mode=2, rows=32)] * 16 + dense, slots
+
+    _run_steps(dev, seqs, attn, cache, 3, descs, seed=33 + int(with_dense))

@@ -100,6 +100,8 @@ __global__ __launch_bounds__(1024) void step_build_kernel(StepBuildArgs a) {
   __shared__ int s_keep[kStepMaxSeq], s_sbase[kStepMaxSeq], s_pages[kStepMaxSeq];
   __shared__ int s_wlo[kStepMaxSeq], s_wn[kStepMaxSeq], s_woff[kStepMaxSeq];
   __shared__ int s_dense_rows[kStepMaxSeq];  // rows of a full-attention sequence, -1 otherwise
+  __shared__ int s_npages[kStepMaxSeq];
+  __shared__ int s_srange[kStepMaxSeq], s_sseq[kStepMaxSeq];  // slot ranges in slot order: start, sequence
   __shared__ int s_scan[16 * 8];
   const int i = threadIdx.x;
   const bool live = i < a.n;
@@ -173,6 +175,7 @@ __global__ __launch_bounds__(1024) void step_build_kernel(StepBuildArgs a) {
     s_keep[i] = (mode == 1 || mode == 2) ? keep : 0;
     s_sbase[i] = sbase;
     s_pages[i] = a.page_off[i];
+    s_npages[i] = a.page_off[i + 1] - a.page_off[i];
     s_wlo[i] = wlo;
     s_wn[i] = wn;
     s_woff[i] = woff;
@@ -181,6 +184,12 @@ __global__ __launch_bounds__(1024) void step_build_kernel(StepBuildArgs a) {
     if (mode == 2) {
       a.cached_ids[c_at] = i;
       a.slot_off[c_at] = sbase;
+      s_srange[c_at] = sbase;
+      s_sseq[c_at] = i;
+    }
+    if (mode == 1) {
+      s_srange[n_cached + j_at] = sbase;
+      s_sseq[n_cached + j_at] = i;
     }
     if (mode == 1) {
       int32_t* j = a.jobs + kJobCols * (int64_t)j_at;
@@ -228,19 +237,35 @@ __global__ __launch_bounds__(1024) void step_build_kernel(StepBuildArgs a) {
     a.dense_ids[rank] = i;
   }
   if (!fits) return;  // uniform: the host sizes the buffers from the same state
-  for (int q = 0; q < a.n; ++q) {
-    const int r0 = s_cu[q], nr = s_rows[q], st = s_start[q];
-    for (int t = threadIdx.x; t < nr; t += blockDim.x) {
-      a.positions[r0 + t] = st + t;
-      a.token_index[r0 + t] = (int64_t)q * a.tok_stride + st + t;
+  // Per-row, per-slot and per-window arrays, each flattened over the whole
+  // batch: element e belongs to the last sequence (range) whose start is
+  // <= e, found by binary search over the starts in LDS (all starts are in
+  // ascending order; empty ranges are skipped by taking the last match).
+  auto owner = [&](const int* starts, int n, int e) {
+    int lo = 0, hi = n - 1;  // starts[0] <= e
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (starts[mid] <= e) lo = mid; else hi = mid - 1;
     }
-    const int nk = s_keep[q], sb = s_sbase[q], po = s_pages[q], np = a.page_off[q + 1] - po;
-    for (int r = threadIdx.x; r < nk; r += blockDim.x) {
-      const int pg = r >> 8;
-      a.slots[sb + r] = pg < np ? a.pages[po + pg] * 256 + (r & 255) : -1;
-    }
-    const int wo = s_woff[q], wl = s_wn[q], h0 = r0 + s_wlo[q] - st;
-    for (int t = threadIdx.x; t < wl; t += blockDim.x) a.smp_rows[wo + t] = h0 + t;
+    return lo;
+  };
+  for (int e = threadIdx.x; e < tot_rows; e += blockDim.x) {
+    const int q = owner(s_cu, a.n, e);
+    const int t = e - s_cu[q], st = s_start[q];
+    a.positions[e] = st + t;
+    a.token_index[e] = (int64_t)q * a.tok_stride + st + t;
+  }
+  const int n_ranges = n_cached + n_job;
+  for (int e = threadIdx.x; e < tot_slots; e += blockDim.x) {
+    const int k = owner(s_srange, n_ranges, e);
+    const int q = s_sseq[k];
+    const int r = e - s_srange[k];
+    const int pg = r >> 8;
+    a.slots[e] = pg < s_npages[q] ? a.pages[s_pages[q] + pg] * 256 + (r & 255) : -1;
+  }
+  for (int e = threadIdx.x; e < tot_win; e += blockDim.x) {
+    const int q = owner(s_woff, a.n, e);
+    a.smp_rows[e] = s_cu[q] + s_wlo[q] - s_start[q] + (e - s_woff[q]);
   }
 }
 

@@ -382,32 +382,44 @@ __device__ void find_bin(const uint32_t* hist, int nk, int cum0, int* out) {
   }
 }
 
-// Bitonic sort, descending, of one 32-bit value per thread over the first n
-// threads (n a power of two <= 1024; the other threads hold values sorted
-// among themselves).  Strides below 64 exchange within the wavefront by
-// lane permutes; larger ones go through `xchg` (1024 words of LDS).
-__device__ uint32_t bitonic_desc_reg(uint32_t x, int n, uint32_t* xchg) {
-  const int p = threadIdx.x;
-  for (int kk = 2; kk <= n; kk <<= 1) {
+// Rank of every key among up to 1024 unique 32-bit keys, one per thread
+// (threads without a key hold 0, which ranks below every real key): each
+// wavefront sorts its 64 keys descending with lane shuffles (21 stages), the
+// sorted runs go to `runs` (1024 words of LDS), and a key's rank is its lane
+// in its own run plus, for each of the other 15 runs, the number of its keys
+// that are larger -- a 7-probe binary search (65 possible counts), the 15
+// searches advancing in lockstep.  Returns the rank of the key the thread holds after the wave sort
+// (rank = position in the descending order); *key receives that key.
+__device__ int rank_sort_desc(uint32_t x, uint32_t* runs, uint32_t* key) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int kk = 2; kk <= 64; kk <<= 1) {
     for (int jj = kk >> 1; jj > 0; jj >>= 1) {
-      uint32_t y;
-      if (jj >= 64) {
-        __syncthreads();
-        xchg[p] = x;
-        __syncthreads();
-        y = xchg[p ^ jj];
-      } else {
-        y = (uint32_t)__shfl_xor((int)x, jj);
-      }
-      const bool low = (p & jj) == 0, desc = (p & kk) == 0;
+      const uint32_t y = (uint32_t)__shfl_xor((int)x, jj);
+      const bool low = (lane & jj) == 0, desc = (lane & kk) == 0;
       x = (low == desc) ? max(x, y) : min(x, y);
     }
   }
-  return x;
+  runs[threadIdx.x] = x;
+  __syncthreads();
+  constexpr int kRuns = kTopkThreads / 64;
+  // runs are descending, so the keys > x form a prefix: its length is built
+  // from the bits 32 .. 1 (at most 63), then the last key decides 64
+  int cnt[kRuns];
+#pragma unroll
+  for (int r = 0; r < kRuns; ++r) cnt[r] = 0;
+#pragma unroll
+  for (int b = 32; b >= 1; b >>= 1)
+#pragma unroll
+    for (int r = 0; r < kRuns; ++r) cnt[r] += runs[r * 64 + cnt[r] + b - 1] > x ? b : 0;
+  int rank = lane;
+#pragma unroll
+  for (int r = 0; r < kRuns; ++r) rank += r == wave ? 0 : cnt[r] + (runs[r * 64 + 63] > x ? 1 : 0);
+  *key = x;
+  return rank;
 }
 
 constexpr int kLdsCand = 16384;  // candidates whose raw scores and order keys stay in LDS
-constexpr int kRegSort = 1024;   // selected rows sorted one per thread in registers
+constexpr int kRegSort = 1024;   // selected rows ranked one per thread (rank_sort_desc)
 
 // bf16 bits of the raw score of candidate u before the division by sqrt(D): the
 // stored group maximum (head_select), or bf16 of the KV heads' partial sums added
@@ -550,12 +562,12 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(SelArgs a) {
     __syncthreads();
     int32_t* selc = reinterpret_cast<int32_t*>(pool);  // rank -> candidate (raw bits / keys are dead)
     if (P2 <= kRegSort) {
-      uint32_t x = tid < nk ? skey[tid] : 0u;  // 0 sorts below every real key
-      x = bitonic_desc_reg(x, P2, sh.chunk);
-      if (tid < nk) {
+      uint32_t x;
+      const int rank = rank_sort_desc(tid < nk ? skey[tid] : 0u, sh.chunk, &x);  // 0 ranks below every real key
+      if (x != 0u) {  // exactly the nk real keys
         const int c = 0xffff - (int)(x & 0xffffu);
-        selc[tid] = c;
-        if (io) io[tid] = c;
+        selc[rank] = c;
+        if (io) io[rank] = c;
       }
     } else {
       for (int i = nk + tid; i < P2; i += blockDim.x) skey[i] = 0u;

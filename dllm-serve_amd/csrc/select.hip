@@ -126,6 +126,35 @@ __device__ int block_excount(bool flag, int* wave_tot, int* total) {
   return base + below;
 }
 
+// Exclusive prefix sums of two per-thread counts over the workgroup
+// (wavefronts in order), both in one pass.  Every thread must call it.
+__device__ void block_exscan2(int a, int b, int* wave_tot2, int* ex_a, int* ex_b) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  int xa = a, xb = b;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int ya = __shfl_up(xa, off), yb = __shfl_up(xb, off);
+    if (lane >= off) {
+      xa += ya;
+      xb += yb;
+    }
+  }
+  __syncthreads();
+  if (lane == 63) {
+    wave_tot2[2 * wave] = xa;
+    wave_tot2[2 * wave + 1] = xb;
+  }
+  __syncthreads();
+  int ba = 0, bb = 0;
+  for (int w = 0; w < wave; ++w) {
+    ba += wave_tot2[2 * w];
+    bb += wave_tot2[2 * w + 1];
+  }
+  *ex_a = ba + xa - a;
+  *ex_b = bb + xb - b;
+}
+
 // ---- 1. scores ---------------------------------------------------------------
 // grid (ceil(max_kc / 256), Hkv, n_job), block 256, dynamic LDS = 64 KiB of K
 // rows + the g query heads' qbar as f32.  K rows: 16 lanes per 256-byte row,
@@ -293,6 +322,7 @@ struct TopkShared {
   int start[257];
   int running[256];
   int wave_tot[16];
+  int wave_tot2[2 * 16];
   uint32_t chunk[kTopkThreads];
   int misc[4];  // threshold search results: high byte, count above it, low byte, count above T
 };
@@ -542,20 +572,33 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(SelArgs a) {
     __syncthreads();
     const uint32_t T = (hb << 8) | (uint32_t)sh.misc[2];
     const int need_eq = nk - sh.misc[3];  // ties at T to take, lowest indices first
-    // index-order compaction; unique keys: score key, then the complement of the candidate
-    int run_eq = 0, run_pos = 0;
-    for (int b0 = 0; b0 < kc; b0 += kTopkThreads) {
-      const int c = b0 + tid;
-      const uint32_t key = c < kc ? okl[c] : 0u;
-      const bool gt = c < kc && key > T;
-      const bool eq = c < kc && key == T;
-      int eq_tot, sel_tot;
-      const int er = block_excount(eq, sh.wave_tot, &eq_tot) + run_eq;
-      const bool take = gt || (eq && er < need_eq);
-      const int pos = block_excount(take, sh.wave_tot, &sel_tot) + run_pos;
-      if (take) skey[pos] = (key << 16) | (uint32_t)(0xffff - c);
-      run_eq += eq_tot;
-      run_pos += sel_tot;
+    // Index-order compaction (unique keys: score key, then the complement of
+    // the candidate).  Thread t owns the E consecutive candidates from E t;
+    // one scan gives the counts of better (> T) and tied (== T) candidates
+    // before them, and a kept candidate goes to position
+    // (better before it) + min(tied before it, need_eq).
+    const int E = (kc + kTopkThreads - 1) / kTopkThreads;
+    const int c0 = tid * E;
+    int ngt = 0, neq = 0;
+    for (int e = 0; e < E; ++e) {
+      const int c = c0 + e;
+      if (c < kc) {
+        const uint32_t key = okl[c];
+        ngt += key > T;
+        neq += key == T;
+      }
+    }
+    int gt_before, eq_before;
+    block_exscan2(ngt, neq, sh.wave_tot2, &gt_before, &eq_before);
+    for (int e = 0; e < E; ++e) {
+      const int c = c0 + e;
+      if (c >= kc) break;
+      const uint32_t key = okl[c];
+      const bool gt = key > T, eq = key == T;
+      if (gt || (eq && eq_before < need_eq))
+        skey[gt_before + min(eq_before, need_eq)] = (key << 16) | (uint32_t)(0xffff - c);
+      gt_before += gt;
+      eq_before += eq;
     }
     int P2 = 1;
     while (P2 < nk) P2 <<= 1;

@@ -362,12 +362,13 @@ def bench_select(dev, n_layers=4):
     return out
 
 
-def bench_sparse_c4(dev, steps_block=64, quick=False, n_layers=8):
+def bench_sparse_c4(dev, steps_block=64, quick=False, n_layers=32):
     """C4 attention per 64-step block and per layer (B=4, P=1024, gen 256,
-    block 64, LLaDA shape): sparse = head_select retention 0.5 (1 full step,
-    1 full step + selection/store, 62 reuse steps); dense = 64 full recompute
-    steps.  Each step runs n_layers layers (own q/k/v and cache pages each);
-    the figure is the block's time divided by n_layers.
+    block 64, LLaDA-8B shape): sparse = head_select retention 0.5 (1 full
+    step, 1 full step + selection/store, 62 reuse steps); dense = 64 full
+    recompute steps.  Each step runs the model's 32 attention layers (own
+    q/k/v and cache pages each), so the per-step table work is shared as in
+    the model; the figure is the block's time divided by n_layers.
 
     Primary figures: the steps as the device-step path runs them -- each
     step's tables built on the device and the step replayed from a HIP graph

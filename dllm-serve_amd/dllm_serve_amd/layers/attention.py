@@ -33,10 +33,24 @@ from ..sparse.state import keep_count
 from ..utils.context import get_context
 
 
-def _check_rows(t: torch.Tensor, name: str) -> None:
-    if t.dim() != 3 or t.stride(-1) != 1 or t.stride(1) != t.shape[2]:
+def _token_rows(t: torch.Tensor, heads: int, head_dim: int, name: str):
+    """(t, rows, token stride in elements) of q/k/v given as [rows, heads *
+    head_dim] or [rows, heads, head_dim] with contiguous heads; any other
+    shape goes through the reference's ``view(-1, heads, head_dim)``."""
+    sh = t.shape
+    if len(sh) == 2 and sh[1] == heads * head_dim:
+        st = t.stride()
+        if st[1] != 1:
+            raise ValueError(f"{name} must have contiguous heads; got shape {tuple(sh)} strides {st}")
+        return t, sh[0], st[0]
+    if len(sh) != 3 or sh[1] != heads or sh[2] != head_dim:
+        t = t.view(-1, heads, head_dim)
+        sh = t.shape
+    st = t.stride()
+    if st[2] != 1 or st[1] != head_dim:
         raise ValueError(f"{name} must be [rows, heads, head_dim] with contiguous heads; got shape "
-                         f"{tuple(t.shape)} strides {t.stride()}")
+                         f"{tuple(sh)} strides {st}")
+    return t, sh[0], st[0]
 
 
 def _slot_tensor(slot_mapping, device) -> torch.Tensor:
@@ -228,6 +242,7 @@ class StepPlan:
         for k in self._SCALARS:
             setattr(self, k, getattr(lay, k))
         self._ws = {}
+        self._args = {}
         self.last_idx = None
 
     @classmethod
@@ -248,6 +263,21 @@ class StepPlan:
             self._ws[key] = t
         return t
 
+    def launch_args(self, Hq: int, Hkv: int, D: int) -> dict:
+        """Device addresses of the step's tables and the K3b workspace for
+        one head shape, computed once per step for all layers."""
+        key = (Hq, Hkv, D)
+        a = self._args.get(key)
+        if a is None:
+            ws = self.workspace("cached", _capi.block_cached_workspace_size(
+                self.n_cached, self.max_q_cached, self.max_keys_cached, Hq, Hkv, D)) if self.n_cached else None
+            a = dict(cu=self.cu.data_ptr(), slots=self.slots.data_ptr(), slot_off=self.slot_off.data_ptr(),
+                     dense_ids=None if self.dense_identity else self.dense_ids.data_ptr(),
+                     cached_ids=None if self.cached_identity else self.cached_ids.data_ptr(),
+                     ws=None if ws is None else ws.data_ptr(), ws_bytes=0 if ws is None else ws.numel())
+            self._args[key] = a
+        return a
+
 
 class Attention(nn.Module):
     """Drop-in for dllmserve.layers.attention.Attention (attention.py:95-119)."""
@@ -264,11 +294,12 @@ class Attention(nn.Module):
         self.k_cache = self.v_cache = torch.tensor([])
         self.layer_id = None
         self.last_select_indices = None
+        self._cache_ok = None  # (tensors, addresses, sizes) of the last bound cache that passed _check_cache
 
     def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
-        q = q.view(-1, self.num_heads, self.head_dim)
-        k = k.view(-1, self.num_kv_heads, self.head_dim)
-        v = v.view(-1, self.num_kv_heads, self.head_dim)
+        # q/k/v as [rows, heads * head_dim] or [rows, heads, head_dim] are used
+        # without the reference's view (attention.py:108-110); other shapes
+        # take that view
         context = get_context()
         if context.is_diffusion:
             return self._mixed_sparse_dense_attention(q, k, v, context)
@@ -283,53 +314,72 @@ class Attention(nn.Module):
             context._dllm_plan = plan
         return plan
 
-    def _check_cache(self, device) -> None:
-        # the kernels address the bound cache as flat bf16 rows of Hkv * head_dim
-        # elements on q's device (the checks store_kvcache makes, attention.py:42-47)
-        for t, n in ((self.k_cache, "k_cache"), (self.v_cache, "v_cache")):
+    def _check_cache(self, device) -> tuple:
+        """Check the bound cache and return (k address, v address, slots).
+        The kernels address it as flat bf16 rows of Hkv * head_dim elements on
+        q's device (the checks store_kvcache makes, attention.py:42-47); a
+        cache that passed keeps passing while the same tensors keep their
+        addresses and sizes."""
+        kc, vc = self.k_cache, self.v_cache
+        key = (kc, vc, kc.data_ptr(), vc.data_ptr(), kc.numel(), vc.numel(), device)
+        ok = self._cache_ok
+        if ok is not None and ok[0] is kc and ok[1] is vc and ok[2:7] == key[2:]:
+            return ok[7]
+        for t, n in ((kc, "k_cache"), (vc, "v_cache")):
             if (t.dtype != torch.bfloat16 or not t.is_contiguous() or t.device != device or t.dim() < 2
                     or tuple(t.shape[-2:]) != (self.num_kv_heads, self.head_dim)):
                 raise ValueError(f"{n} must be a contiguous bf16 tensor [..., {self.num_kv_heads}, {self.head_dim}] "
                                  f"on {device}; got {t.dtype} {tuple(t.shape)} on {t.device}")
+        res = (kc.data_ptr(), vc.data_ptr(), min(kc.numel(), vc.numel()) // (self.num_kv_heads * self.head_dim))
+        self._cache_ok = key + (res,)
+        return res
 
     def _mixed_sparse_dense_attention(self, q, k, v, context):
-        for t, n in ((q, "q"), (k, "k"), (v, "v")):
-            _check_rows(t, n)
+        Hq, Hkv, D = self.num_heads, self.num_kv_heads, self.head_dim
+        q, nq, q_st = _token_rows(q, Hq, D, "q")
+        k, nk, k_st = _token_rows(k, Hkv, D, "k")
+        v, nv, v_st = _token_rows(v, Hkv, D, "v")
         if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
             raise TypeError(f"bf16 q/k/v expected, got {q.dtype}/{k.dtype}/{v.dtype}")
-        if not q.is_cuda:
+        if not (q.is_cuda and k.is_cuda and v.is_cuda):
             raise RuntimeError("Attention runs on the GPU only (no CPU fallback)")
-        plan = self._plan(context, q.device)
-        if q.shape[0] != plan.total_rows or k.shape[0] != plan.total_rows or v.shape[0] != plan.total_rows:
-            raise ValueError(f"q/k/v have {q.shape[0]}/{k.shape[0]}/{v.shape[0]} rows, the step's sequences "
-                             f"feed {plan.total_rows}")
+        if not (k.get_device() == v.get_device() == q.get_device()):
+            raise ValueError(f"q/k/v are on different devices: {q.device}/{k.device}/{v.device}")
+        dev = q.device
+        plan = self._plan(context, dev)
+        if nq != plan.total_rows or nk != plan.total_rows or nv != plan.total_rows:
+            raise ValueError(f"q/k/v have {nq}/{nk}/{nv} rows, the step's sequences feed {plan.total_rows}")
         o = torch.zeros_like(q) if plan.any_skipped else torch.empty_like(q)
-        Hq, Hkv, D = self.num_heads, self.num_kv_heads, self.head_dim
+        o_st = o.stride(0)
+        args = plan.launch_args(Hq, Hkv, D)
+        stream = _capi._stream(dev)
+        qp, kp, vp, op = q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr()
 
         if plan.n_dense:
-            ids = None if plan.dense_identity else plan.dense_ids
-            _capi.attn_varlen_fwd(q, k, v, o, plan.cu, plan.cu, ids, plan.n_dense, plan.max_q_dense, self.scale)
+            _capi.attn_varlen_fwd_raw(qp, kp, vp, op, args["cu"], args["dense_ids"], plan.n_dense, plan.max_q_dense,
+                                      Hq, Hkv, D, q_st, k_st, v_st, o_st, float(self.scale), stream)
 
         if plan.n_job:
             if not (self.k_cache.numel() and self.v_cache.numel()):
                 raise RuntimeError("cache state 1 needs k_cache/v_cache bound to this layer")
-            self._check_cache(q.device)
+            self._check_cache(dev)
             ws = plan.workspace("select", _capi.select_workspace_size(plan.n_job, plan.max_kc, Hq, Hkv, D))
             idx = None
             if self.keep_indices:
-                idx = torch.full((plan.n_job, Hkv, plan.max_keep), -1, dtype=torch.int64, device=q.device)
-            _capi.select_kv_store(q, k, v, plan.jobs, plan.n_job, plan.max_kc, plan.max_keep, np.float32(D ** 0.5),
+                idx = torch.full((plan.n_job, Hkv, plan.max_keep), -1, dtype=torch.int64, device=dev)
+            q3 = q if q.dim() == 3 else q.view(-1, Hq, D)
+            k3 = k if k.dim() == 3 else k.view(-1, Hkv, D)
+            v3 = v if v.dim() == 3 else v.view(-1, Hkv, D)
+            _capi.select_kv_store(q3, k3, v3, plan.jobs, plan.n_job, plan.max_kc, plan.max_keep, np.float32(D ** 0.5),
                                   self.k_cache, self.v_cache, plan.slots, idx, ws)
             self.last_select_indices = idx
 
         if plan.n_cached:
             if not (self.k_cache.numel() and self.v_cache.numel()):
                 raise RuntimeError("cache state 2 needs k_cache/v_cache bound to this layer")
-            self._check_cache(q.device)
-            ws = plan.workspace("cached", _capi.block_cached_workspace_size(
-                plan.n_cached, plan.max_q_cached, plan.max_keys_cached, Hq, Hkv, D))
-            ids = None if plan.cached_identity else plan.cached_ids
-            _capi.attn_block_cached_fwd(q, k, v, o, plan.cu, ids, plan.n_cached, plan.max_q_cached, plan.max_keys_cached,
-                                        self.k_cache, self.v_cache, plan.slots, plan.slot_off,
-                                        self.scale, ws)
-        return o.view(-1, Hq * D)
+            kc, vc, cache_slots = self._check_cache(dev)
+            _capi.attn_block_cached_fwd_raw(qp, kp, vp, op, args["cu"], args["cached_ids"], plan.n_cached,
+                                            plan.max_q_cached, plan.max_keys_cached, kc, vc, cache_slots,
+                                            args["slots"], args["slot_off"], Hq, Hkv, D, q_st, k_st, v_st, o_st,
+                                            float(self.scale), args["ws"], args["ws_bytes"], stream)
+        return o if o.dim() == 2 else o.view(-1, Hq * D)

@@ -36,7 +36,8 @@ namespace dllm {
 
 constexpr int SHD = 128;           // the head dim these kernels handle
 constexpr int kJobCols = 8;        // row0, n_tok, blk_start, blk_len, n_keep, slot_off, head_select, pool_k
-constexpr int kScoreCands = 256;   // candidates per score workgroup
+constexpr int kScoreCands = 256;   // candidates per score workgroup (one per thread)
+constexpr int kScoreCandsMax = 304;  // per workgroup when that saves a second generation (see the launch)
 constexpr int kQbarStage = 32768;  // bytes of block rows staged per qbar chunk (inside the K-tile area)
 constexpr int kTopkThreads = 1024;
 constexpr int kSortCap = 8192;     // selected rows sorted in LDS as 64-bit keys
@@ -59,6 +60,7 @@ struct SelArgs {
   int64_t n_slots;
   int64_t* idx_out;  // [n_job][Hkv][max_keep] or null
   int n_part;        // top-k workgroups per (job, KV head): each selects, then copies 1/n_part of the rows
+  int score_cpw;     // candidates per score workgroup: a multiple of 16 in [kScoreCands, kScoreCandsMax]
   // workspace
   uint16_t* raw;     // [n_job][Hkv][max_kc] bf16 bits (head_select jobs)
   double* part;      // [n_job][Hkv][max_kc] per-KV-head sums (token-selection jobs)
@@ -156,8 +158,9 @@ __device__ void block_exscan2(int a, int b, int* wave_tot2, int* ex_a, int* ex_b
 }
 
 // ---- 1. scores ---------------------------------------------------------------
-// grid (ceil(max_kc / 256), Hkv, n_job), block 256, dynamic LDS = 64 KiB of K
-// rows + the g query heads' qbar as f32.  K rows: 16 lanes per 256-byte row,
+// grid (ceil(max_kc / cpw), Hkv, n_job), block 256, dynamic LDS = cpw rows of
+// K (256 bytes each; cpw = 256, or up to 304 with threads taking a second
+// candidate) + the g query heads' qbar as f32.  K rows: 16 lanes per 256-byte row,
 // stored with 16-byte chunk c at c ^ (row & 15) so that the per-lane row reads
 // afterwards (lane = row) spread over all banks.
 // qbar[h][d] = bf16(f32(f64 sum_t q[bs+t][h][d] / bl)), t ascending: the
@@ -170,18 +173,20 @@ __device__ void block_exscan2(int a, int b, int* wave_tot2, int* ex_a, int* ex_b
 __global__ __launch_bounds__(256) void score_kernel(SelArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   uint8_t* kt = lds;
-  float* qs = reinterpret_cast<float*>(lds + kScoreCands * 256);
+  const int cpw = a.score_cpw;
+  float* qs = reinterpret_cast<float*>(lds + cpw * 256);
   const int jid = blockIdx.z;
   const int kv = blockIdx.y;
   const Job jb = load_job(a, jid);
-  const int c0 = blockIdx.x * kScoreCands;
+  const int c0 = blockIdx.x * cpw;
   if (c0 >= jb.kc) return;
   const int g = a.g;
   const int tid = threadIdx.x;
   const int rsub = tid >> 4, ch = tid & 15;
-  u32x4_t rows[kScoreCands / 16];
+  u32x4_t rows[kScoreCandsMax / 16];
 #pragma unroll
-  for (int p = 0; p < kScoreCands / 16; ++p) {
+  for (int p = 0; p < kScoreCandsMax / 16; ++p) {
+    if (16 * p >= cpw) break;  // uniform
     const int c = c0 + 16 * p + rsub;
     const int64_t row = (int64_t)jb.row0 + cand_row(jb, min(c, jb.kc - 1));
     rows[p] = ld128(a.k + row * a.k_stride + (int64_t)kv * SHD + ch * 8);
@@ -242,17 +247,20 @@ __global__ __launch_bounds__(256) void score_kernel(SelArgs a) {
     __syncthreads();  // the stage area becomes the K tile
   }
 #pragma unroll
-  for (int p = 0; p < kScoreCands / 16; ++p) {
+  for (int p = 0; p < kScoreCandsMax / 16; ++p) {
+    if (16 * p >= cpw) break;
     const int r = 16 * p + rsub;
     *reinterpret_cast<u32x4_t*>(kt + r * 256 + ((ch ^ (r & 15)) << 4)) = rows[p];
   }
   __syncthreads();
-  const int c = c0 + tid;
+  // thread tid scores candidates tid and tid + 256 (the latter when cpw > 256)
+  for (int cl0 = tid; cl0 < cpw; cl0 += 256) {
+  const int c = c0 + cl0;
   if (c >= jb.kc) return;
-  // lane tid reads row tid; physical chunk cl ^ (tid & 15) (the 16 lanes of a
+  // lane reads row cl0; physical chunk cl ^ (cl0 & 15) (the 16 lanes of a
   // read group hit 16 different chunks)
-  const uint8_t* krow = kt + tid * 256;
-  const int sw = tid & 15;
+  const uint8_t* krow = kt + cl0 * 256;
+  const int sw = cl0 & 15;
   const int64_t out = ((int64_t)jid * a.Hkv + kv) * a.max_kc + c;
   float best = -INFINITY;
   double part = 0.0;
@@ -275,6 +283,7 @@ __global__ __launch_bounds__(256) void score_kernel(SelArgs a) {
     a.raw[out] = (uint16_t)(__float_as_uint(best) >> 16);
   else
     a.part[out] = part;
+  }
 }
 
 // ---- 2. top-k and copy ------------------------------------------------------------------
@@ -803,11 +812,28 @@ extern "C" int dllm_select_kv_store(const dllm_bf16* q, const dllm_bf16* k, cons
     a.cidx1 = reinterpret_cast<int32_t*>(ws + o); o += L.cidx;
   }
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  const size_t score_lds = (size_t)kScoreCands * 256 + (size_t)a.g * SHD * sizeof(float);
+  // Two score workgroups fit per CU (VGPRs, and LDS up to 80 KiB each): when
+  // 256 candidates per workgroup need more than one such generation on the
+  // 256 CUs and up to 304 fit in one, take the larger workgroups (4 x 1280
+  // tokens, 32 KV heads: 640 -> 512 workgroups; the last 128 ran as a second
+  // generation).
+  const size_t qs_bytes = (size_t)a.g * SHD * sizeof(float);
+  const int64_t heads = (int64_t)Hkv * n_job;
+  a.score_cpw = kScoreCands;
+  {
+    const int64_t n1 = (max_kc + kScoreCands - 1) / kScoreCands;
+    const int64_t n2 = (max_kc + kScoreCandsMax - 1) / kScoreCandsMax;
+    if (n1 * heads > 512 && n2 < n1 && n2 * heads <= 512) {
+      const int cpw = (int)(((max_kc + n2 - 1) / n2 + 15) / 16 * 16);
+      if ((size_t)cpw * 256 + qs_bytes <= 80 * 1024) a.score_cpw = cpw;
+    }
+  }
+  const size_t score_lds = (size_t)a.score_cpw * 256 + qs_bytes;
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(score_kernel),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)score_lds);
   if (e != hipSuccess) return fail(DLLM_ERR_HIP, "%s: hipFuncSetAttribute: %s", name, hipGetErrorString(e));
-  score_kernel<<<dim3((max_kc + kScoreCands - 1) / kScoreCands, Hkv, n_job), dim3(256), score_lds, st>>>(a);
+  score_kernel<<<dim3((unsigned)((max_kc + a.score_cpw - 1) / a.score_cpw), Hkv, n_job), dim3(256), score_lds, st>>>(
+      a);
   int rc = check_launch(name);
   if (rc) return rc;
   // enough top-k workgroups to give every CU one (256 CUs), at most four per (job, KV head)

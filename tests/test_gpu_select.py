@@ -191,6 +191,38 @@ def test_select_c4_four_jobs(dev):
     assert np.array_equal(bits(cd[1]).reshape(-1, Hkv * D), ref_vc)
 
 
+def test_select_wide_score_workgroups_ragged(dev):
+    """Four jobs of 32 KV heads with 1216 / 1100 / 1000 / 1210 candidates:
+    256 candidates per score workgroup would need 5 x 32 x 4 = 640 workgroups
+    (more than the 512 that fit at once), so the launch takes 304 per
+    workgroup (threads 0..47 score a second candidate) -- with partly filled
+    last workgroups here, head and token selection mixed."""
+    print("select wide score workgroups, ragged", flush=True)
+    Hq = Hkv = 32
+    lens = [(1280, 1024, 64, 0.5, 1, 3), (1164, 900, 64, 0.5, 0, 3), (1064, 1000, 64, 0.25, 1, 5),
+            (1274, 0, 64, 0.5, 1, 1)]
+    n = sum(x[0] for x in lens)
+    q, k, v = _inputs(n, Hq, Hkv, seed=304)
+    specs, row0, soff = [], 0, 0
+    for n_tok, bs, bl, r, hs, pk in lens:
+        nk = keep_count(n_tok - bl, r)
+        specs.append((row0, n_tok, bs, bl, nk, soff, hs, pk))
+        row0 += n_tok
+        soff += nk
+    assert max(s[1] - s[3] for s in specs) == 1216
+    pages = -(-soff // 256) + 1
+    slots = torch.randperm(pages * 256, generator=torch.Generator().manual_seed(5))[:soff].to(torch.int32)
+    cache = torch.zeros(2, pages * 256, Hkv, D, dtype=torch.bfloat16)
+    ref_kc, ref_vc = bits(cache[0]).reshape(-1, Hkv * D).copy(), bits(cache[1]).reshape(-1, Hkv * D).copy()
+    refs = [_expected(q, k, v, sp, ref_kc, ref_vc, slots.numpy()) for sp in specs]
+    cd = cache.to(dev)
+    got, _, _ = _run_jobs(dev, q.to(dev), k.to(dev), v.to(dev), specs, cd[0], cd[1], slots.to(dev))
+    for j, (sp, ref) in enumerate(zip(specs, refs)):
+        _check(got[j], ref, sp, f"job {j}")
+    assert np.array_equal(bits(cd[0]).reshape(-1, Hkv * D), ref_kc)
+    assert np.array_equal(bits(cd[1]).reshape(-1, Hkv * D), ref_vc)
+
+
 def test_select_mixed_configs_one_launch(dev):
     """Jobs of one launch with head_select True / False and pool 1 / 3 / 5 and
     different ratios (each SparseConfig read per sequence, attention.py:211,

@@ -160,7 +160,8 @@ __device__ void block_exscan2(int a, int b, int* wave_tot2, int* ex_a, int* ex_b
 // ---- 1. scores ---------------------------------------------------------------
 // grid (ceil(max_kc / cpw), Hkv, n_job), block 256, dynamic LDS = cpw rows of
 // K (256 bytes each; cpw = 256, or up to 304 with threads taking a second
-// candidate) + the g query heads' qbar as f32.  K rows: 16 lanes per 256-byte row,
+// candidate) + the g query heads' qbar as f32 (padded to a multiple of four
+// heads when g > 1).  K rows: 16 lanes per 256-byte row,
 // stored with 16-byte chunk c at c ^ (row & 15) so that the per-lane row reads
 // afterwards (lane = row) spread over all banks.
 // qbar[h][d] = bf16(f32(f64 sum_t q[bs+t][h][d] / bl)), t ascending: the
@@ -264,20 +265,48 @@ __global__ __launch_bounds__(256) void score_kernel(SelArgs a) {
   const int64_t out = ((int64_t)jid * a.Hkv + kv) * a.max_kc + c;
   float best = -INFINITY;
   double part = 0.0;
-  for (int gi = 0; gi < g; ++gi) {
-    const float* qq = qs + gi * SHD;
+  if (g == 1) {
     double acc = 0.0;
 #pragma unroll 4
     for (int cl = 0; cl < 16; ++cl) {
       const u32x4_t x = *reinterpret_cast<const u32x4_t*>(krow + ((cl ^ sw) << 4));
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
-        acc = __builtin_fma((double)qq[8 * cl + 2 * w], (double)bf16_val(x[w] & 0xffffu), acc);
-        acc = __builtin_fma((double)qq[8 * cl + 2 * w + 1], (double)bf16_val(x[w] >> 16), acc);
+        acc = __builtin_fma((double)qs[8 * cl + 2 * w], (double)bf16_val(x[w] & 0xffffu), acc);
+        acc = __builtin_fma((double)qs[8 * cl + 2 * w + 1], (double)bf16_val(x[w] >> 16), acc);
       }
     }
-    best = fmaxf(best, bf16_val(f64_to_bf16_bits_2step(acc)));
-    part += acc;
+    best = bf16_val(f64_to_bf16_bits_2step(acc));
+    part = acc;
+  } else {
+    // four query heads at a time, their dependent f64 chains interleaved
+    // (each head still sums d ascending); the heads of the group below g are
+    // folded into best / part in ascending order
+    for (int g0 = 0; g0 < g; g0 += 4) {
+      const int gn = min(4, g - g0);
+      double acc[4] = {0.0, 0.0, 0.0, 0.0};
+      const float* qq = qs + g0 * SHD;
+#pragma unroll 2
+      for (int cl = 0; cl < 16; ++cl) {
+        const u32x4_t x = *reinterpret_cast<const u32x4_t*>(krow + ((cl ^ sw) << 4));
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const double k0 = (double)bf16_val(x[w] & 0xffffu), k1 = (double)bf16_val(x[w] >> 16);
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {  // heads past g read the padding of qs and are not folded in
+            acc[u] = __builtin_fma((double)qq[u * SHD + 8 * cl + 2 * w], k0, acc[u]);
+            acc[u] = __builtin_fma((double)qq[u * SHD + 8 * cl + 2 * w + 1], k1, acc[u]);
+          }
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        if (u < gn) {
+          best = fmaxf(best, bf16_val(f64_to_bf16_bits_2step(acc[u])));
+          part += acc[u];
+        }
+      }
+    }
   }
   if (jb.head_select)
     a.raw[out] = (uint16_t)(__float_as_uint(best) >> 16);
@@ -817,7 +846,8 @@ extern "C" int dllm_select_kv_store(const dllm_bf16* q, const dllm_bf16* k, cons
   // 256 CUs and up to 304 fit in one, take the larger workgroups (4 x 1280
   // tokens, 32 KV heads: 640 -> 512 workgroups; the last 128 ran as a second
   // generation).
-  const size_t qs_bytes = (size_t)a.g * SHD * sizeof(float);
+  // qbar of g heads, padded to a multiple of four (the dot products run four heads at a time)
+  const size_t qs_bytes = (size_t)(a.g == 1 ? 1 : (a.g + 3) / 4 * 4) * SHD * sizeof(float);
   const int64_t heads = (int64_t)Hkv * n_job;
   a.score_cpw = kScoreCands;
   {

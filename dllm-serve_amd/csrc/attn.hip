@@ -739,30 +739,37 @@ __device__ __forceinline__ void cached_tile(const uint8_t* Ks, const uint8_t* Vs
 // in VGPRs (with a budget of 512 the compiler moves the O^T accumulators
 // between AGPRs and VGPRs around every softmax rescale).
 template <int RB>
-__global__ __launch_bounds__(256 * RB) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_cached_kernel(AttnArgs a) {
+// The launch geometry and the tables the first, dependent loads read come as
+// leading scalar arguments (14 dwords): the library is built with kernel
+// argument preloading, so they are in SGPRs when a wave starts instead of one
+// scalar load away (the rest of AttnArgs is loaded as usual).
+__global__ __launch_bounds__(256 * RB) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_cached_kernel(
+    const int32_t* __restrict__ slot_off, const int32_t* __restrict__ seg_ids, const int32_t* __restrict__ cu_q,
+    const int32_t* __restrict__ slots, int xcd_chunk, int logical_blocks, int mtiles, int n_split, int Hkv,
+    int keys_per_split, AttnArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   constexpr int NJ = 8 / RB;  // K (and V) DMA instructions per wavefront per tile
-  const int L = xcd_remap(blockIdx.x, a.xcd_chunk);
-  if (L >= a.logical_blocks) return;
-  const int mblocks = (a.mtiles + RB - 1) / RB;
+  const int L = xcd_remap(blockIdx.x, xcd_chunk);
+  if (L >= logical_blocks) return;
+  const int mblocks = (mtiles + RB - 1) / RB;
   int r = L;
-  const int split = r % a.n_split;
-  r /= a.n_split;
+  const int split = r % n_split;
+  r /= n_split;
   const int mb = r % mblocks;
   r /= mblocks;
-  const int hkv = r % a.Hkv;
-  const int s = r / a.Hkv;
+  const int hkv = r % Hkv;
+  const int s = r / Hkv;
   // The slot list of segment s needs slot_off only: its first fetches are
   // issued before the segment's rows (cu_q, possibly behind seg_ids) are
   // known, so that those two dependent loads overlap.
   // (The scalar loads of the segment's offsets all come first: a load after
   // the first DMA into LDS could no longer be a scalar one.)
-  const int slot_base = a.slot_off[s];
-  const int n_c = a.slot_off[s + 1] - slot_base;
-  const int kbeg0 = split * a.keys_per_split;  // this split's first key (past Lk: no tiles)
-  const int sid = a.seg_ids ? a.seg_ids[s] : s;
-  const int qrow0 = a.cu_q[sid];
-  const int Lq = a.cu_q[sid + 1] - qrow0;
+  const int slot_base = slot_off[s];
+  const int n_c = slot_off[s + 1] - slot_base;
+  const int kbeg0 = split * keys_per_split;  // this split's first key (past Lk: no tiles)
+  const int sid = seg_ids ? seg_ids[s] : s;
+  const int qrow0 = cu_q[sid];
+  const int Lq = cu_q[sid + 1] - qrow0;
 
   const int tid = threadIdx.x;
   const int wave_id = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -780,11 +787,11 @@ __global__ __launch_bounds__(256 * RB) __attribute__((amdgpu_waves_per_eu(2, 2))
   // 32 w + 4j + rl; K chunk (P ^ rl) ^ 4(j & 3), V chunk P ^ 4 rl.
   const uint32_t kchunk = (uint32_t)((P ^ rl) * 16);
   const uint32_t vchunk = (uint32_t)((P ^ (4 * rl)) * 16);
-  const int64_t row_elems = (int64_t)a.Hkv * HD;
+  const int64_t row_elems = (int64_t)Hkv * HD;
   // without a cache (cache_slots = 0, slots may be null) every cached row is
   // outside it: the fetches then read slot_off[0], a valid dummy
-  const bool have_slots = n_c > 0 && a.slots != nullptr && a.cache_slots > 0;
-  const int32_t* sp = have_slots ? a.slots + slot_base : a.slot_off;
+  const bool have_slots = n_c > 0 && slots != nullptr && a.cache_slots > 0;
+  const int32_t* sp = have_slots ? slots + slot_base : slot_off;
   // Per-wave pipeline: the slots of tile t+2 are fetched before tile t+1's
   // DMA is issued, so that after computing tile t the wave can issue tile
   // t+2 into the stage it just freed while tile t+1 is still in flight --
@@ -826,7 +833,7 @@ __global__ __launch_bounds__(256 * RB) __attribute__((amdgpu_waves_per_eu(2, 2))
   }
   const int Lk = n_c + Lq;
   const int kbeg = min(kbeg0, Lk);
-  const int kend = min(Lk, kbeg + a.keys_per_split);
+  const int kend = min(Lk, kbeg + keys_per_split);
   // Rows past kend read the last valid row; a cached row with an invalid
   // slot reads block row 0 (never the cache, which may be absent).  Both are
   // masked out of the softmax, so only the address needs to be valid.
@@ -1198,11 +1205,15 @@ static int block_cached_impl(const char* name, const dllm_bf16* q, const dllm_bf
   if (rb == 2) {
     constexpr int lds_bytes = ck_lds_bytes(2);
     if ((rc = set_lds(attn_cached_kernel<2>, lds_bytes, name))) return rc;
-    attn_cached_kernel<2><<<dim3(nb), dim3(512), lds_bytes, st>>>(a);
+    attn_cached_kernel<2><<<dim3(nb), dim3(512), lds_bytes, st>>>(a.slot_off, a.seg_ids, a.cu_q, a.slots, a.xcd_chunk,
+                                                                  a.logical_blocks, a.mtiles, a.n_split, a.Hkv,
+                                                                  a.keys_per_split, a);
   } else {
     constexpr int lds_bytes = ck_lds_bytes(1);
     if ((rc = set_lds(attn_cached_kernel<1>, lds_bytes, name))) return rc;
-    attn_cached_kernel<1><<<dim3(nb), dim3(256), lds_bytes, st>>>(a);
+    attn_cached_kernel<1><<<dim3(nb), dim3(256), lds_bytes, st>>>(a.slot_off, a.seg_ids, a.cu_q, a.slots, a.xcd_chunk,
+                                                                  a.logical_blocks, a.mtiles, a.n_split, a.Hkv,
+                                                                  a.keys_per_split, a);
   }
   if ((rc = check_launch(name))) return rc;
   if (n_split > 1) {

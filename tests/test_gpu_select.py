@@ -223,6 +223,43 @@ def test_select_wide_score_workgroups_ragged(dev):
     assert np.array_equal(bits(cd[1]).reshape(-1, Hkv * D), ref_vc)
 
 
+def test_select_wide_score_workgroups_gqa(dev):
+    """28 query / 4 KV heads, 32 jobs of up to 1216 candidates: 5 x 4 x 32 =
+    640 score workgroups of 256 would need a second generation, so the launch
+    takes 304 candidates per workgroup with qbar padded from 7 to 8 heads
+    (the dot products run four heads at a time); ragged jobs, head and token
+    selection."""
+    print("select wide score workgroups, GQA 28/4, 32 jobs", flush=True)
+    Hq, Hkv = 28, 4
+    rng = np.random.default_rng(28)
+    lens = []
+    for j in range(32):
+        n_tok = int(rng.integers(1000, 1281)) if j else 1280
+        bl = 64
+        bs = int(rng.integers(0, n_tok - bl + 1))
+        lens.append((n_tok, bs, bl, 0.5, j % 2, (1, 3, 5)[j % 3]))
+    n = sum(x[0] for x in lens)
+    q, k, v = _inputs(n, Hq, Hkv, seed=2804)
+    specs, row0, soff = [], 0, 0
+    for n_tok, bs, bl, r, hs, pk in lens:
+        nk = keep_count(n_tok - bl, r)
+        specs.append((row0, n_tok, bs, bl, nk, soff, hs, pk))
+        row0 += n_tok
+        soff += nk
+    assert max(s[1] - s[3] for s in specs) == 1216
+    pages = -(-soff // 256) + 1
+    slots = torch.randperm(pages * 256, generator=torch.Generator().manual_seed(6))[:soff].to(torch.int32)
+    cache = torch.zeros(2, pages * 256, Hkv, D, dtype=torch.bfloat16)
+    ref_kc, ref_vc = bits(cache[0]).reshape(-1, Hkv * D).copy(), bits(cache[1]).reshape(-1, Hkv * D).copy()
+    refs = [_expected(q, k, v, sp, ref_kc, ref_vc, slots.numpy()) for sp in specs]
+    cd = cache.to(dev)
+    got, _, _ = _run_jobs(dev, q.to(dev), k.to(dev), v.to(dev), specs, cd[0], cd[1], slots.to(dev))
+    for j, (sp, ref) in enumerate(zip(specs, refs)):
+        _check(got[j], ref, sp, f"job {j}")
+    assert np.array_equal(bits(cd[0]).reshape(-1, Hkv * D), ref_kc)
+    assert np.array_equal(bits(cd[1]).reshape(-1, Hkv * D), ref_vc)
+
+
 def test_select_mixed_configs_one_launch(dev):
     """Jobs of one launch with head_select True / False and pool 1 / 3 / 5 and
     different ratios (each SparseConfig read per sequence, attention.py:211,

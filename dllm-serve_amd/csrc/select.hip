@@ -519,29 +519,31 @@ __device__ __forceinline__ void copy_selected(const SelArgs& a, const Job& jb, i
   constexpr int kPer = 8;
   for (int i0 = 0; i0 < n_items; i0 += kPer * kTopkThreads) {
     u32x4_t kx[kPer], vx[kPer];
-    int64_t dst[kPer];
+    int64_t slot[kPer];
+    int64_t e[kPer];
+    // the source rows depend only on the ranks in LDS, the destinations on
+    // the slot list: both loads are issued before either is waited for
 #pragma unroll
     for (int u = 0; u < kPer; ++u) {
       const int i = i0 + u * kTopkThreads + (int)threadIdx.x;
-      dst[u] = -1;
+      slot[u] = -1;
       if (i < n_items) {
         const int r = r0 + (i >> 4), chk = i & 15;
         const int j = cand(r);
-        const int64_t slot = a.slots[jb.slot_off + r];
-        if (slot >= 0 && slot < a.cache_slots && j >= 0 && j < jb.kc) {
+        if (j >= 0 && j < jb.kc) {
           const int64_t row = (int64_t)jb.row0 + cand_row(jb, j);
-          const int64_t e = (int64_t)h * SHD + chk * 8;
-          kx[u] = ld128_stream(a.k + row * a.k_stride + e);
-          vx[u] = ld128_stream(a.v + row * a.v_stride + e);
-          dst[u] = slot * row_elems + e;
+          e[u] = (int64_t)h * SHD + chk * 8;
+          kx[u] = ld128_stream(a.k + row * a.k_stride + e[u]);
+          vx[u] = ld128_stream(a.v + row * a.v_stride + e[u]);
+          slot[u] = a.slots[jb.slot_off + r];
         }
       }
     }
 #pragma unroll
     for (int u = 0; u < kPer; ++u)
-      if (dst[u] >= 0) {
-        st128(a.k_cache + dst[u], kx[u]);
-        st128(a.v_cache + dst[u], vx[u]);
+      if (slot[u] >= 0 && slot[u] < a.cache_slots) {
+        st128(a.k_cache + slot[u] * row_elems + e[u], kx[u]);
+        st128(a.v_cache + slot[u] * row_elems + e[u], vx[u]);
       }
   }
 }

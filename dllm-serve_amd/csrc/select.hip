@@ -254,7 +254,63 @@ __global__ __launch_bounds__(256) void score_kernel(SelArgs a) {
     *reinterpret_cast<u32x4_t*>(kt + r * 256 + ((ch ^ (r & 15)) << 4)) = rows[p];
   }
   __syncthreads();
-  // thread tid scores candidates tid and tid + 256 (the latter when cpw > 256)
+  if (g == 1) {
+    // thread tid scores candidate tid and, in a workgroup of more than 256,
+    // candidate tid + 256: a wavefront with any second candidate runs the two
+    // dependent f64 chains interleaved (each still d ascending; lanes without
+    // a second candidate run a discarded copy on a valid row).  Lane reads row
+    // r at physical chunk cl ^ (r & 15): the 16 lanes of a read group hit 16
+    // different chunks.
+    const int cb = tid + 256;
+    const bool has_a = c0 + tid < jb.kc;
+    const bool has_b = cb < cpw && c0 + cb < jb.kc;
+    const uint8_t* ka = kt + tid * 256;
+    const int swa = tid & 15;
+    double acc_a = 0.0, acc_b = 0.0;
+    if (__builtin_amdgcn_ballot_w64(has_b)) {
+      const int rb = min(cb, cpw - 1);
+      const uint8_t* kb = kt + rb * 256;
+      const int swb = rb & 15;
+#pragma unroll 4
+      for (int cl = 0; cl < 16; ++cl) {
+        const u32x4_t xa = *reinterpret_cast<const u32x4_t*>(ka + ((cl ^ swa) << 4));
+        const u32x4_t xb = *reinterpret_cast<const u32x4_t*>(kb + ((cl ^ swb) << 4));
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const double q0 = (double)qs[8 * cl + 2 * w], q1 = (double)qs[8 * cl + 2 * w + 1];
+          acc_a = __builtin_fma(q0, (double)bf16_val(xa[w] & 0xffffu), acc_a);
+          acc_b = __builtin_fma(q0, (double)bf16_val(xb[w] & 0xffffu), acc_b);
+          acc_a = __builtin_fma(q1, (double)bf16_val(xa[w] >> 16), acc_a);
+          acc_b = __builtin_fma(q1, (double)bf16_val(xb[w] >> 16), acc_b);
+        }
+      }
+    } else if (has_a) {
+#pragma unroll 4
+      for (int cl = 0; cl < 16; ++cl) {
+        const u32x4_t x = *reinterpret_cast<const u32x4_t*>(ka + ((cl ^ swa) << 4));
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          acc_a = __builtin_fma((double)qs[8 * cl + 2 * w], (double)bf16_val(x[w] & 0xffffu), acc_a);
+          acc_a = __builtin_fma((double)qs[8 * cl + 2 * w + 1], (double)bf16_val(x[w] >> 16), acc_a);
+        }
+      }
+    }
+    const int64_t out = ((int64_t)jid * a.Hkv + kv) * a.max_kc + c0 + tid;
+    if (has_a) {
+      if (jb.head_select)
+        a.raw[out] = (uint16_t)(f64_to_bf16_bits_2step(acc_a));
+      else
+        a.part[out] = acc_a;
+    }
+    if (has_b) {
+      if (jb.head_select)
+        a.raw[out + 256] = (uint16_t)(f64_to_bf16_bits_2step(acc_b));
+      else
+        a.part[out + 256] = acc_b;
+    }
+    return;
+  }
+  // g > 1: thread tid scores candidates tid and tid + 256 (the latter when cpw > 256)
   for (int cl0 = tid; cl0 < cpw; cl0 += 256) {
   const int c = c0 + cl0;
   if (c >= jb.kc) return;
@@ -265,20 +321,7 @@ __global__ __launch_bounds__(256) void score_kernel(SelArgs a) {
   const int64_t out = ((int64_t)jid * a.Hkv + kv) * a.max_kc + c;
   float best = -INFINITY;
   double part = 0.0;
-  if (g == 1) {
-    double acc = 0.0;
-#pragma unroll 4
-    for (int cl = 0; cl < 16; ++cl) {
-      const u32x4_t x = *reinterpret_cast<const u32x4_t*>(krow + ((cl ^ sw) << 4));
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        acc = __builtin_fma((double)qs[8 * cl + 2 * w], (double)bf16_val(x[w] & 0xffffu), acc);
-        acc = __builtin_fma((double)qs[8 * cl + 2 * w + 1], (double)bf16_val(x[w] >> 16), acc);
-      }
-    }
-    best = bf16_val(f64_to_bf16_bits_2step(acc));
-    part = acc;
-  } else {
+  {
     // four query heads at a time, their dependent f64 chains interleaved
     // (each head still sums d ascending); the heads of the group below g are
     // folded into best / part in ascending order

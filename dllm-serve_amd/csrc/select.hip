@@ -160,8 +160,8 @@ __device__ void block_exscan2(int a, int b, int* wave_tot2, int* ex_a, int* ex_b
 // ---- 1. scores ---------------------------------------------------------------
 // grid (ceil(max_kc / cpw), Hkv, n_job), block 256, dynamic LDS = cpw rows of
 // K (256 bytes each; cpw = 256, or up to 304 with threads taking a second
-// candidate) + the g query heads' qbar as f32 (padded to a multiple of four
-// heads when g > 1).  K rows: 16 lanes per 256-byte row,
+// candidate) + the g query heads' qbar as f64 (padded to four heads when
+// 1 < g <= 4, to a multiple of eight above).  K rows: 16 lanes per 256-byte row,
 // stored with 16-byte chunk c at c ^ (row & 15) so that the per-lane row reads
 // afterwards (lane = row) spread over all banks.
 // qbar[h][d] = bf16(f32(f64 sum_t q[bs+t][h][d] / bl)), t ascending: the
@@ -171,11 +171,42 @@ __device__ void block_exscan2(int a, int b, int* wave_tot2, int* ex_a, int* ex_b
 // tid % 64) then sums d = 2l and 2l + 1 row by row.
 // dot(h, j) = sum_d qbar[h][d] * k[j][kv][d] in f64, d ascending (each product
 // of two bf16 values is exact in f64, so fma gives the same sums).
+// Dot products of one candidate's K row (LDS, chunk c at c ^ sw) with GW
+// query heads' qbar (f64, [head][d]); heads gn..GW-1 read the padding of qbar
+// and are not folded in.
+template <int GW>
+__device__ __forceinline__ void score_group(const uint8_t* krow, int sw, const double* qq, int gn, float& best,
+                                            double& part) {
+  double acc[GW];
+#pragma unroll
+  for (int u = 0; u < GW; ++u) acc[u] = 0.0;
+#pragma unroll 2
+  for (int cl = 0; cl < 16; ++cl) {
+    const u32x4_t x = *reinterpret_cast<const u32x4_t*>(krow + ((cl ^ sw) << 4));
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const double k0 = (double)bf16_val(x[w] & 0xffffu), k1 = (double)bf16_val(x[w] >> 16);
+#pragma unroll
+      for (int u = 0; u < GW; ++u) {
+        acc[u] = __builtin_fma(qq[u * SHD + 8 * cl + 2 * w], k0, acc[u]);
+        acc[u] = __builtin_fma(qq[u * SHD + 8 * cl + 2 * w + 1], k1, acc[u]);
+      }
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < GW; ++u) {
+    if (u < gn) {
+      best = fmaxf(best, bf16_val(f64_to_bf16_bits_2step(acc[u])));
+      part += acc[u];
+    }
+  }
+}
+
 __global__ __launch_bounds__(256) void score_kernel(SelArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   uint8_t* kt = lds;
   const int cpw = a.score_cpw;
-  float* qs = reinterpret_cast<float*>(lds + cpw * 256);
+  double* qs = reinterpret_cast<double*>(lds + cpw * 256);
   const int jid = blockIdx.z;
   const int kv = blockIdx.y;
   const Job jb = load_job(a, jid);
@@ -241,8 +272,8 @@ __global__ __launch_bounds__(256) void score_kernel(SelArgs a) {
         }
       }
       if (hs < hp) {
-        qs[(h0 + hs) * SHD + 2 * l] = bf16_val(f64_to_bf16_bits_2step(s0 / (double)jb.bl));
-        qs[(h0 + hs) * SHD + 2 * l + 1] = bf16_val(f64_to_bf16_bits_2step(s1 / (double)jb.bl));
+        qs[(h0 + hs) * SHD + 2 * l] = (double)bf16_val(f64_to_bf16_bits_2step(s0 / (double)jb.bl));
+        qs[(h0 + hs) * SHD + 2 * l + 1] = (double)bf16_val(f64_to_bf16_bits_2step(s1 / (double)jb.bl));
       }
     }
     __syncthreads();  // the stage area becomes the K tile
@@ -277,7 +308,7 @@ __global__ __launch_bounds__(256) void score_kernel(SelArgs a) {
         const u32x4_t xb = *reinterpret_cast<const u32x4_t*>(kb + ((cl ^ swb) << 4));
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
-          const double q0 = (double)qs[8 * cl + 2 * w], q1 = (double)qs[8 * cl + 2 * w + 1];
+          const double q0 = qs[8 * cl + 2 * w], q1 = qs[8 * cl + 2 * w + 1];
           acc_a = __builtin_fma(q0, (double)bf16_val(xa[w] & 0xffffu), acc_a);
           acc_b = __builtin_fma(q0, (double)bf16_val(xb[w] & 0xffffu), acc_b);
           acc_a = __builtin_fma(q1, (double)bf16_val(xa[w] >> 16), acc_a);
@@ -290,8 +321,8 @@ __global__ __launch_bounds__(256) void score_kernel(SelArgs a) {
         const u32x4_t x = *reinterpret_cast<const u32x4_t*>(ka + ((cl ^ swa) << 4));
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
-          acc_a = __builtin_fma((double)qs[8 * cl + 2 * w], (double)bf16_val(x[w] & 0xffffu), acc_a);
-          acc_a = __builtin_fma((double)qs[8 * cl + 2 * w + 1], (double)bf16_val(x[w] >> 16), acc_a);
+          acc_a = __builtin_fma(qs[8 * cl + 2 * w], (double)bf16_val(x[w] & 0xffffu), acc_a);
+          acc_a = __builtin_fma(qs[8 * cl + 2 * w + 1], (double)bf16_val(x[w] >> 16), acc_a);
         }
       }
     }
@@ -321,35 +352,14 @@ __global__ __launch_bounds__(256) void score_kernel(SelArgs a) {
   const int64_t out = ((int64_t)jid * a.Hkv + kv) * a.max_kc + c;
   float best = -INFINITY;
   double part = 0.0;
-  {
-    // four query heads at a time, their dependent f64 chains interleaved
-    // (each head still sums d ascending); the heads of the group below g are
-    // folded into best / part in ascending order
-    for (int g0 = 0; g0 < g; g0 += 4) {
-      const int gn = min(4, g - g0);
-      double acc[4] = {0.0, 0.0, 0.0, 0.0};
-      const float* qq = qs + g0 * SHD;
-#pragma unroll 2
-      for (int cl = 0; cl < 16; ++cl) {
-        const u32x4_t x = *reinterpret_cast<const u32x4_t*>(krow + ((cl ^ sw) << 4));
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          const double k0 = (double)bf16_val(x[w] & 0xffffu), k1 = (double)bf16_val(x[w] >> 16);
-#pragma unroll
-          for (int u = 0; u < 4; ++u) {  // heads past g read the padding of qs and are not folded in
-            acc[u] = __builtin_fma((double)qq[u * SHD + 8 * cl + 2 * w], k0, acc[u]);
-            acc[u] = __builtin_fma((double)qq[u * SHD + 8 * cl + 2 * w + 1], k1, acc[u]);
-          }
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        if (u < gn) {
-          best = fmaxf(best, bf16_val(f64_to_bf16_bits_2step(acc[u])));
-          part += acc[u];
-        }
-      }
-    }
+  // GW query heads at a time (4, or 8 when g > 4), their dependent f64
+  // chains interleaved (each head still sums d ascending) and every K element
+  // converted once for the group; the heads of the group below g are folded
+  // into best / part in ascending order
+  if (g > 4) {
+    for (int g0 = 0; g0 < g; g0 += 8) score_group<8>(krow, sw, qs + g0 * SHD, min(8, g - g0), best, part);
+  } else {
+    score_group<4>(krow, sw, qs, g, best, part);
   }
   if (jb.head_select)
     a.raw[out] = (uint16_t)(__float_as_uint(best) >> 16);
@@ -891,8 +901,9 @@ extern "C" int dllm_select_kv_store(const dllm_bf16* q, const dllm_bf16* k, cons
   // 256 CUs and up to 304 fit in one, take the larger workgroups (4 x 1280
   // tokens, 32 KV heads: 640 -> 512 workgroups; the last 128 ran as a second
   // generation).
-  // qbar of g heads, padded to a multiple of four (the dot products run four heads at a time)
-  const size_t qs_bytes = (size_t)(a.g == 1 ? 1 : (a.g + 3) / 4 * 4) * SHD * sizeof(float);
+  // qbar of g heads as f64, padded to four heads (g <= 4) or to a multiple of eight (the dot products'
+  // head groups)
+  const size_t qs_bytes = (size_t)(a.g == 1 ? 1 : a.g > 4 ? (a.g + 7) / 8 * 8 : 4) * SHD * sizeof(double);
   const int64_t heads = (int64_t)Hkv * n_job;
   a.score_cpw = kScoreCands;
   {

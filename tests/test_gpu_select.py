@@ -123,6 +123,16 @@ def test_select_beyond_8192_candidates(dev, n_tok, bs, bl, Hq, Hkv, ratio, head_
     _one_job(dev, n_tok, bs, bl, Hq, Hkv, ratio, head_select, pool_k, seed=n_tok + Hkv)
 
 
+@pytest.mark.parametrize("Hq,Hkv", [(6, 2), (10, 2), (12, 2), (24, 3), (16, 1), (64, 1)])
+@pytest.mark.parametrize("head_select", [True, False])
+def test_select_group_sizes(dev, Hq, Hkv, head_select):
+    """Query heads per KV head g = 3 (one padded group of four), 5, 6 and 8 (one group of eight),
+    16 (two groups) and 64 (the largest group the launch takes): the score kernel's head groups and
+    the qbar padding, bit-exact in both selection modes."""
+    print(f"select group size g={Hq // Hkv} Hq={Hq} Hkv={Hkv} hs={head_select}", flush=True)
+    _one_job(dev, 360, 200, 24, Hq, Hkv, 0.5, head_select, 3, seed=Hq * 7 + Hkv)
+
+
 def test_select_summation_order(dev):
     """Scores whose f64 sums are inexact, so the order of the additions decides
     the result: q rows of one token (qbar = q exactly) hold +-2^60 at

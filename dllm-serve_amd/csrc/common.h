@@ -81,6 +81,51 @@ __device__ __forceinline__ float pair_sum32(float x) {
   return __builtin_bit_cast(float, (uint32_t)r[0]) + __builtin_bit_cast(float, (uint32_t)r[1]);
 }
 
+// Cross-lane moves inside the LDS-free VALU datapath (DPP and the gfx950
+// permlane swaps) instead of ds_bpermute round trips; every lane of the
+// wavefront must be active.  Lane semantics (checked on the device): row_shl:n
+// gives lane l the value of lane l + n of its 16-lane row, row_shr:n of lane
+// l - n (0 past the row start with bound_ctrl), row_ror:8 of lane l ^ 8,
+// row_bcast:15 / :31 of lane 15 / 31 to the rows selected by the row mask;
+// permlane16_swap(x, x) returns rows (0, 0, 2, 2) and (1, 1, 3, 3) of x,
+// permlane32_swap(x, x) halves (0, 0) and (1, 1).
+__device__ __forceinline__ uint32_t lane_xor(uint32_t x, int j) {
+  const int lane = threadIdx.x & 63;
+  switch (j) {
+    case 1:
+      return (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+    case 2:
+      return (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+    case 4: {
+      const uint32_t up = (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, 0x104, 0xF, 0xF, false);  // l + 4
+      const uint32_t dn = (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, 0x114, 0xF, 0xF, false);  // l - 4
+      return (lane & 4) ? dn : up;
+    }
+    case 8:
+      return (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, 0x128, 0xF, 0xF, false);  // row_ror:8
+    case 16: {
+      const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+      return (lane & 16) ? (uint32_t)r[0] : (uint32_t)r[1];
+    }
+    default: {
+      const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+      return (lane & 32) ? (uint32_t)r[0] : (uint32_t)r[1];
+    }
+  }
+}
+
+// Inclusive prefix sum over the 64 lanes: sums within 16-lane rows
+// (row_shr 1, 2, 4, 8), then the row totals carried by row_bcast.
+__device__ __forceinline__ int wave_incl_scan(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, true);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, true);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, true);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, true);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false);
+  return x;
+}
+
 // Plain 128-bit global load / store.
 __device__ __forceinline__ u32x4_t ld128(const void* p) { return *reinterpret_cast<const u32x4_t*>(p); }
 

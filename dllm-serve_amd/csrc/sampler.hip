@@ -59,9 +59,9 @@ __device__ __forceinline__ void smx_merge(float& m, float& s, int& i, float m2, 
 __device__ __forceinline__ void smx_wave_reduce(float& m, float& s, int& i) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) {
-    const float m2 = __shfl_xor(m, off);
-    const float s2 = __shfl_xor(s, off);
-    const int i2 = __shfl_xor(i, off);
+    const float m2 = __uint_as_float(lane_xor(__float_as_uint(m), off));
+    const float s2 = __uint_as_float(lane_xor(__float_as_uint(s), off));
+    const int i2 = (int)lane_xor((uint32_t)i, off);
     smx_merge(m, s, i, m2, s2, i2);
   }
 }
@@ -209,7 +209,7 @@ __device__ void smx_finish(const SmxArgs& a, int row, float m, float s, int idx)
       }
     }
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) found = min(found, __shfl_xor(found, off));
+    for (int off = 32; off >= 1; off >>= 1) found = min(found, (int)lane_xor((uint32_t)found, off));
     best = min(best, found);
   }
   if (lane == 0) {
@@ -251,7 +251,7 @@ __device__ __forceinline__ uint32_t conf_order(uint32_t b) {
 
 __device__ __forceinline__ int block_sum(int v, int* red) {
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+  for (int off = 32; off >= 1; off >>= 1) v += (int)lane_xor((uint32_t)v, off);
   __syncthreads();
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
   __syncthreads();

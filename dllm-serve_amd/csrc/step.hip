@@ -67,15 +67,7 @@ __device__ void block_exscan_n(const int (&v)[N], int (&ex)[N], int (&tot)[N], i
   const int wave = threadIdx.x >> 6;
   int x[N];
 #pragma unroll
-  for (int n = 0; n < N; ++n) x[n] = v[n];
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-#pragma unroll
-    for (int n = 0; n < N; ++n) {
-      const int y = __shfl_up(x[n], off);
-      if (lane >= off) x[n] += y;
-    }
-  }
+  for (int n = 0; n < N; ++n) x[n] = wave_incl_scan(v[n]);
   if (lane == 63)
 #pragma unroll
     for (int n = 0; n < N; ++n) lds[wave * N + n] = x[n];

@@ -208,8 +208,12 @@ __device__ void smx_finish(const SmxArgs& a, int row, float m, float s, int idx)
         if (j < idx && f >= thr && f32_to_bf16_bits(expf(f - m) / s) == P) found = min(found, j);
       }
     }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) found = min(found, (int)lane_xor((uint32_t)found, off));
+    found = min(found, (int)lane_xor((uint32_t)found, 32));
+    found = min(found, (int)lane_xor((uint32_t)found, 16));
+    found = min(found, (int)lane_xor((uint32_t)found, 8));
+    found = min(found, (int)lane_xor((uint32_t)found, 4));
+    found = min(found, (int)lane_xor((uint32_t)found, 2));
+    found = min(found, (int)lane_xor((uint32_t)found, 1));
     best = min(best, found);
   }
   if (lane == 0) {

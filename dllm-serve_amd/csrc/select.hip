@@ -490,15 +490,38 @@ __device__ void find_bin(const uint32_t* hist, int nk, int cum0, int* out) {
   }
 }
 
+// The rank of key x among the first NR descending runs of 64 keys in `runs`:
+// its lane in its own run plus, for each other run, the number of its keys
+// that are larger.  The keys > x form a prefix of a run: its length is built
+// from the bits 32 .. 1 (at most 63), then the last key decides 64; the NR
+// searches advance in lockstep.
+template <int NR>
+__device__ __forceinline__ int rank_search(uint32_t x, const uint32_t* runs, int lane, int wave) {
+  int cnt[NR];
+#pragma unroll
+  for (int r = 0; r < NR; ++r) cnt[r] = 0;
+#pragma unroll
+  for (int b = 32; b >= 1; b >>= 1)
+#pragma unroll
+    for (int r = 0; r < NR; ++r) cnt[r] += runs[r * 64 + cnt[r] + b - 1] > x ? b : 0;
+  int rank = lane;
+#pragma unroll
+  for (int r = 0; r < NR; ++r) rank += r == wave ? 0 : cnt[r] + (runs[r * 64 + 63] > x ? 1 : 0);
+  return rank;
+}
+
 // Rank of every key among up to 1024 unique 32-bit keys, one per thread
 // (threads without a key hold 0, which ranks below every real key): each
-// wavefront sorts its 64 keys descending with DPP / permlane moves (21 stages), the
-// sorted runs go to `runs` (1024 words of LDS), and a key's rank is its lane
-// in its own run plus, for each of the other 15 runs, the number of its keys
-// that are larger -- a 7-probe binary search (65 possible counts), the 15
-// searches advancing in lockstep.  Returns the rank of the key the thread holds after the wave sort
-// (rank = position in the descending order); *key receives that key.
-__device__ int rank_sort_desc(uint32_t x, uint32_t* runs, uint32_t* key) {
+// wavefront sorts its 64 keys descending with DPP / permlane moves (21
+// stages), the sorted runs go to `runs` (1024 words of LDS), and
+// rank_search counts, for every other run, its keys above the thread's.  The
+// real keys are the first n_keys threads' (ceil(n_keys / 64) runs): the
+// later runs hold only zeros and count nothing, so the search stops at the
+// next multiple of four runs, and wavefronts without a real key return at
+// once.  Returns the rank of the key the thread holds after the wave sort
+// (its position in the descending order; meaningful only for a real key);
+// *key receives that key.
+__device__ int rank_sort_desc(uint32_t x, int n_keys, uint32_t* runs, uint32_t* key) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
   for (int kk = 2; kk <= 64; kk <<= 1) {
@@ -511,21 +534,16 @@ __device__ int rank_sort_desc(uint32_t x, uint32_t* runs, uint32_t* key) {
   }
   runs[threadIdx.x] = x;
   __syncthreads();
-  constexpr int kRuns = kTopkThreads / 64;
-  // runs are descending, so the keys > x form a prefix: its length is built
-  // from the bits 32 .. 1 (at most 63), then the last key decides 64
-  int cnt[kRuns];
-#pragma unroll
-  for (int r = 0; r < kRuns; ++r) cnt[r] = 0;
-#pragma unroll
-  for (int b = 32; b >= 1; b >>= 1)
-#pragma unroll
-    for (int r = 0; r < kRuns; ++r) cnt[r] += runs[r * 64 + cnt[r] + b - 1] > x ? b : 0;
-  int rank = lane;
-#pragma unroll
-  for (int r = 0; r < kRuns; ++r) rank += r == wave ? 0 : cnt[r] + (runs[r * 64 + 63] > x ? 1 : 0);
   *key = x;
-  return rank;
+  constexpr int kRuns = kTopkThreads / 64;
+  const int nruns = (n_keys + 63) >> 6;  // wave-uniform
+  if (wave >= nruns) return 0;
+  // the search covers the first NR runs, NR the multiple of four at or above
+  // nruns (the runs between hold only zeros)
+  if (nruns <= 4) return rank_search<4>(x, runs, lane, wave);
+  if (nruns <= 8) return rank_search<8>(x, runs, lane, wave);
+  if (nruns <= 12) return rank_search<12>(x, runs, lane, wave);
+  return rank_search<kRuns>(x, runs, lane, wave);
 }
 
 constexpr int kLdsCand = 16384;  // candidates whose raw scores and order keys stay in LDS
@@ -688,7 +706,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(SelArgs a) {
     int32_t* selc = reinterpret_cast<int32_t*>(pool);  // rank -> candidate (raw bits / keys are dead)
     if (P2 <= kRegSort) {
       uint32_t x;
-      const int rank = rank_sort_desc(tid < nk ? skey[tid] : 0u, sh.chunk, &x);  // 0 ranks below every real key
+      const int rank = rank_sort_desc(tid < nk ? skey[tid] : 0u, nk, sh.chunk, &x);  // 0 ranks below every real key
       if (x != 0u) {  // exactly the nk real keys
         const int c = 0xffff - (int)(x & 0xffffu);
         selc[rank] = c;

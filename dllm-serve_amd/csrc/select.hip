@@ -646,59 +646,68 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(SelArgs a) {
     __syncthreads();
     // pooled, scaled order keys (max over the window clipped to the
     // candidates, then bf16(f32 / f32(sqrt D)): monotone, so pooling before
-    // or after the division gives the same value) and the high-byte histogram
+    // or after the division gives the same value) and the high-byte histogram.
+    // When every candidate is kept (n_keep == kc) there is no threshold: the
+    // sort keys go straight to position c, the compaction's index order.
+    const bool keep_all = nk >= kc;
     for (int c = tid; c < kc; c += blockDim.x) {
       const int lo = pk > 1 ? max(0, c - pad) : c;
       const int hi = pk > 1 ? min(kc - 1, c - pad + pk - 1) : c;
       float m = -INFINITY;
       for (int u = lo; u <= hi; ++u) m = fmaxf(m, bf16_val(rawl[u]));
       const uint32_t key = bf16_order_key(f32_to_bf16_bits(m / a.sqrt_d));
-      okl[c] = (uint16_t)key;
-      atomicAdd(&sh.hist[key >> 8], 1u);
-    }
-    __syncthreads();
-    find_bin(sh.hist, nk, 0, sh.misc);
-    __syncthreads();
-    const uint32_t hb = (uint32_t)sh.misc[0];
-    const int above_hb = sh.misc[1];
-    for (int b = tid; b < 256; b += blockDim.x) sh.hist[b] = 0;
-    __syncthreads();
-    for (int c = tid; c < kc; c += blockDim.x) {
-      const uint32_t key = okl[c];
-      if ((key >> 8) == hb) atomicAdd(&sh.hist[key & 255], 1u);
-    }
-    __syncthreads();
-    find_bin(sh.hist, nk, above_hb, sh.misc + 2);
-    __syncthreads();
-    const uint32_t T = (hb << 8) | (uint32_t)sh.misc[2];
-    const int need_eq = nk - sh.misc[3];  // ties at T to take, lowest indices first
-    // Index-order compaction (unique keys: score key, then the complement of
-    // the candidate).  Thread t owns the E consecutive candidates from E t;
-    // one scan gives the counts of better (> T) and tied (== T) candidates
-    // before them, and a kept candidate goes to position
-    // (better before it) + min(tied before it, need_eq).
-    const int E = (kc + kTopkThreads - 1) / kTopkThreads;
-    const int c0 = tid * E;
-    int ngt = 0, neq = 0;
-    for (int e = 0; e < E; ++e) {
-      const int c = c0 + e;
-      if (c < kc) {
-        const uint32_t key = okl[c];
-        ngt += key > T;
-        neq += key == T;
+      if (keep_all) {
+        skey[c] = (key << 16) | (uint32_t)(0xffff - c);
+      } else {
+        okl[c] = (uint16_t)key;
+        atomicAdd(&sh.hist[key >> 8], 1u);
       }
     }
-    int gt_before, eq_before;
-    block_exscan2(ngt, neq, sh.wave_tot2, &gt_before, &eq_before);
-    for (int e = 0; e < E; ++e) {
-      const int c = c0 + e;
-      if (c >= kc) break;
-      const uint32_t key = okl[c];
-      const bool gt = key > T, eq = key == T;
-      if (gt || (eq && eq_before < need_eq))
-        skey[gt_before + min(eq_before, need_eq)] = (key << 16) | (uint32_t)(0xffff - c);
-      gt_before += gt;
-      eq_before += eq;
+    if (!keep_all) {
+      __syncthreads();
+      find_bin(sh.hist, nk, 0, sh.misc);
+      __syncthreads();
+      const uint32_t hb = (uint32_t)sh.misc[0];
+      const int above_hb = sh.misc[1];
+      for (int b = tid; b < 256; b += blockDim.x) sh.hist[b] = 0;
+      __syncthreads();
+      for (int c = tid; c < kc; c += blockDim.x) {
+        const uint32_t key = okl[c];
+        if ((key >> 8) == hb) atomicAdd(&sh.hist[key & 255], 1u);
+      }
+      __syncthreads();
+      find_bin(sh.hist, nk, above_hb, sh.misc + 2);
+      __syncthreads();
+      const uint32_t T = (hb << 8) | (uint32_t)sh.misc[2];
+      const int need_eq = nk - sh.misc[3];  // ties at T to take, lowest indices first
+      // Index-order compaction (unique keys: score key, then the complement of
+      // the candidate).  Thread t owns the E consecutive candidates from E t;
+      // one scan gives the counts of better (> T) and tied (== T) candidates
+      // before them, and a kept candidate goes to position
+      // (better before it) + min(tied before it, need_eq).
+      const int E = (kc + kTopkThreads - 1) / kTopkThreads;
+      const int c0 = tid * E;
+      int ngt = 0, neq = 0;
+      for (int e = 0; e < E; ++e) {
+        const int c = c0 + e;
+        if (c < kc) {
+          const uint32_t key = okl[c];
+          ngt += key > T;
+          neq += key == T;
+        }
+      }
+      int gt_before, eq_before;
+      block_exscan2(ngt, neq, sh.wave_tot2, &gt_before, &eq_before);
+      for (int e = 0; e < E; ++e) {
+        const int c = c0 + e;
+        if (c >= kc) break;
+        const uint32_t key = okl[c];
+        const bool gt = key > T, eq = key == T;
+        if (gt || (eq && eq_before < need_eq))
+          skey[gt_before + min(eq_before, need_eq)] = (key << 16) | (uint32_t)(0xffff - c);
+        gt_before += gt;
+        eq_before += eq;
+      }
     }
     int P2 = 1;
     while (P2 < nk) P2 <<= 1;

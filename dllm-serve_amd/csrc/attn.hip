@@ -119,12 +119,6 @@ __device__ __forceinline__ void vm_wait() {
   asm volatile("" ::: "memory");
 }
 
-// Workgroup barrier between wavefronts that each waited for their own DMA
-// (vm_wait) and finished their own LDS reads: the wait on LDS reads plus
-// s_barrier is all the ordering needed.  __syncthreads() in a kernel that
-// fills LDS with global_load_lds makes the compiler wait for vmcnt(0) before
-// the barrier, which would also retire the DMA of the next tile.
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // AUX = 2: non-temporal (streaming) policy, for bytes that one workgroup reads once.
 template <int AUX = 0>

@@ -126,6 +126,16 @@ __device__ __forceinline__ int wave_incl_scan(int x) {
   return x;
 }
 
+// Workgroup barrier that orders LDS only: each wavefront waits for its own
+// LDS operations, then all meet.  Global loads still in flight stay in flight
+// (the attention kernels' DMA waited for with vm_wait, the selection copy's
+// preloaded rows).  Between wavefronts that each waited for their own DMA
+// (vm_wait) and finished their own LDS reads: the wait on LDS reads plus
+// s_barrier is all the ordering needed.  __syncthreads() in a kernel that
+// fills LDS with global_load_lds makes the compiler wait for vmcnt(0) before
+// the barrier, which would also retire the DMA of the next tile.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // Plain 128-bit global load / store.
 __device__ __forceinline__ u32x4_t ld128(const void* p) { return *reinterpret_cast<const u32x4_t*>(p); }
 

@@ -533,7 +533,7 @@ __device__ int rank_sort_desc(uint32_t x, int n_keys, uint32_t* runs, uint32_t* 
     }
   }
   runs[threadIdx.x] = x;
-  __syncthreads();
+  lds_barrier();  // global loads in flight (the copy's preloaded rows) stay in flight
   *key = x;
   constexpr int kRuns = kTopkThreads / 64;
   const int nruns = (n_keys + 63) >> 6;  // wave-uniform
@@ -714,13 +714,84 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(SelArgs a) {
     __syncthreads();
     int32_t* selc = reinterpret_cast<int32_t*>(pool);  // rank -> candidate (raw bits / keys are dead)
     if (P2 <= kRegSort) {
+      // Part p copies compaction positions [p0, p1) (each selected row once
+      // over the parts).  Its first kPre items per thread are loaded before
+      // the ranks are known, so that their latency overlaps the rank sort,
+      // whose barriers wait on LDS only; a destination needs the row's rank
+      // (rank_of, by candidate) and the rank's slot (slot_l).
+      uint16_t* rank_of = reinterpret_cast<uint16_t*>(pool + 32 * 1024);  // the order keys are dead
+      int32_t* slot_l = selc;                                              // the raw bits are dead
+      const int p0 = (int)((int64_t)nk * part / a.n_part), p1 = (int)((int64_t)nk * (part + 1) / a.n_part);
+      const int n_items = (p1 - p0) * 16;
+      constexpr int kPre = 6;
+      // the slot of rank tid (n_keep <= 1024 here), issued before the rows so
+      // that waiting for it leaves the rows in flight
+      const int32_t my_slot = tid < nk ? a.slots[jb.slot_off + tid] : -1;
+      u32x4_t pk[kPre], pv[kPre];
+      int pc[kPre];
+#pragma unroll
+      for (int u = 0; u < kPre; ++u) {
+        const int i = u * kTopkThreads + tid;
+        pc[u] = -1;
+        if (i < n_items) {
+          const int j = 0xffff - (int)(skey[p0 + (i >> 4)] & 0xffffu);
+          const int64_t row = (int64_t)jb.row0 + cand_row(jb, j);
+          const int64_t e = (int64_t)h * SHD + (i & 15) * 8;
+          pk[u] = ld128_stream(a.k + row * a.k_stride + e);
+          pv[u] = ld128_stream(a.v + row * a.v_stride + e);
+          pc[u] = j;
+        }
+      }
       uint32_t x;
       const int rank = rank_sort_desc(tid < nk ? skey[tid] : 0u, nk, sh.chunk, &x);  // 0 ranks below every real key
       if (x != 0u) {  // exactly the nk real keys
         const int c = 0xffff - (int)(x & 0xffffu);
-        selc[rank] = c;
+        rank_of[c] = (uint16_t)rank;
         if (io) io[rank] = c;
       }
+      if (tid < nk) slot_l[tid] = my_slot;
+      lds_barrier();
+      const int64_t row_elems = (int64_t)a.Hkv * SHD;
+#pragma unroll
+      for (int u = 0; u < kPre; ++u) {
+        if (pc[u] >= 0) {
+          const int64_t slot = slot_l[rank_of[pc[u]]];
+          const int64_t e = (int64_t)h * SHD + ((u * kTopkThreads + tid) & 15) * 8;
+          if (slot >= 0 && slot < a.cache_slots) {
+            st128(a.k_cache + slot * row_elems + e, pk[u]);
+            st128(a.v_cache + slot * row_elems + e, pv[u]);
+          }
+        }
+      }
+      // the rest of the share, eight items per thread in flight
+      constexpr int kPer = 8;
+      for (int i0 = kPre * kTopkThreads; i0 < n_items; i0 += kPer * kTopkThreads) {
+        u32x4_t kx[kPer], vx[kPer];
+        int64_t slot[kPer];
+#pragma unroll
+        for (int u = 0; u < kPer; ++u) {
+          const int i = i0 + u * kTopkThreads + tid;
+          slot[u] = -1;
+          if (i < n_items) {
+            const int j = 0xffff - (int)(skey[p0 + (i >> 4)] & 0xffffu);
+            const int64_t row = (int64_t)jb.row0 + cand_row(jb, j);
+            const int64_t e = (int64_t)h * SHD + (i & 15) * 8;
+            kx[u] = ld128_stream(a.k + row * a.k_stride + e);
+            vx[u] = ld128_stream(a.v + row * a.v_stride + e);
+            slot[u] = slot_l[rank_of[j]];
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < kPer; ++u) {
+          const int i = i0 + u * kTopkThreads + tid;
+          if (slot[u] >= 0 && slot[u] < a.cache_slots) {
+            const int64_t e = (int64_t)h * SHD + (i & 15) * 8;
+            st128(a.k_cache + slot[u] * row_elems + e, kx[u]);
+            st128(a.v_cache + slot[u] * row_elems + e, vx[u]);
+          }
+        }
+      }
+      return;
     } else {
       for (int i = nk + tid; i < P2; i += blockDim.x) skey[i] = 0u;
       __syncthreads();

@@ -71,17 +71,6 @@ __device__ __forceinline__ int xcd_remap(int b, int ch) {
   return (j * 8 + x) * ch + (i - j * ch);
 }
 
-// Buffer resource over [base, base + bytes): loads at offsets >= bytes return
-// zero, which is how rows past the end of a segment read as zero without any
-// per-lane clamping.  The whole offset is passed in the VGPR operand (the
-// scalar offset is kept 0 so the range check covers it); offsets are 32-bit
-// byte offsets from base, which the host checks cannot overflow.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
-}
-__device__ __forceinline__ u32x4_t bload(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-  return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0));
-}
 
 // Running softmax state of one wavefront (M row = lane % 32).  The reference
 // maximum m_run (log2 domain) is only raised when a new score exceeds it by
@@ -107,25 +96,8 @@ constexpr float kLazy = 8.0f;
 // column n (rows 0..3).  With rows = keys and columns = head-dim positions
 // this yields 4 consecutive keys of one d: half of a V^T A-operand fragment.
 
-// s_waitcnt vmcnt(N), expcnt / lgkmcnt untouched (gfx9 encoding: vmcnt bits
-// [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8]).
-// The waitcnt intrinsic is not a memory operation for the compiler, so an
-// empty asm with a memory clobber follows it: no LDS read of the tile being
-// waited for can be hoisted above the wait.
-template <int N>
-__device__ __forceinline__ void vm_wait() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
-  asm volatile("" ::: "memory");
-}
 
 
-// AUX = 2: non-temporal (streaming) policy, for bytes that one workgroup reads once.
-template <int AUX = 0>
-__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint8_t* lds_dst, uint32_t voff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_dst, 16, (int)voff, 0, 0,
-                                           AUX);
-}
 
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ u32x2_t ds_read_tr16(const uint8_t* p) {

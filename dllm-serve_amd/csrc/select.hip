@@ -219,53 +219,95 @@ __global__ __launch_bounds__(256) void score_kernel(SelArgs a) {
     uint32_t* stage = reinterpret_cast<uint32_t*>(kt);  // [row][head of the pass][64 words]
     const int hs = tid >> 6, l = tid & 63;
     const uint16_t* qblk = a.q + ((int64_t)jb.row0 + jb.bs) * a.q_stride + (int64_t)kv * g * SHD;
-    for (int h0 = 0; h0 < g; h0 += 4) {
-      const int hp = min(4, g - h0);             // heads of this pass
-      const int rows_per = kQbarStage / (hp * 256);  // block rows per chunk
-      double s0 = 0.0, s1 = 0.0;
-      for (int t0 = 0; t0 < jb.bl; t0 += rows_per) {
-        const int n = min(rows_per, jb.bl - t0);
-        const int items = n * hp * 16;  // 16-byte pieces of the chunk
-        u32x4_t qv[kQbarStage / (256 * 16)];
+    if ((g * jb.bl + 3) / 4 * 4 <= cpw) {
+      // The whole block fits the K-tile area: all its rows arrive at once by
+      // buffer DMA, [head][row][16 chunks] (instruction j of wave j % 4 fills
+      // 1 KiB = 64 pieces; pieces past the block read as zero), and the heads
+      // are summed in rounds of four from LDS.
+      const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+      const uint32_t qS = (uint32_t)(a.q_stride * 2);
+      const uint32_t qbytes = (uint32_t)(jb.bl - 1) * qS + (uint32_t)(g * SHD * 2);
+      const __amdgpu_buffer_rsrc_t qrs = make_rsrc(qblk, qbytes);
+      const int n_pieces = g * jb.bl * 16;
+      for (int j = wave; j * 64 < n_pieces; j += 4) {
+        const int i = j * 64 + l;
+        const int hr = i >> 4, h = hr / jb.bl, r = hr - h * jb.bl;
+        const uint32_t off = i < n_pieces ? (uint32_t)r * qS + (uint32_t)((h * SHD + (i & 15) * 8) * 2) : qbytes;
+        dma16(qrs, kt + j * 1024, off);
+      }
+      vm_wait<0>();
+      __syncthreads();
+      for (int h = hs; h < g; h += 4) {
+        const uint32_t* sp = stage + h * jb.bl * 64 + l;
+        double s0 = 0.0, s1 = 0.0;
+        int r = 0;
+        for (; r + 16 <= jb.bl; r += 16) {
+          uint32_t w[16];
 #pragma unroll
-        for (int u = 0; u < kQbarStage / (256 * 16); ++u) {
-          const int i = u * 256 + tid;
-          if (i < items) {
-            const int r = i / (hp * 16), rem = i - r * (hp * 16);
-            qv[u] = ld128(qblk + (int64_t)(t0 + r) * a.q_stride + (h0 + (rem >> 4)) * SHD + (rem & 15) * 8);
+          for (int u = 0; u < 16; ++u) w[u] = sp[(r + u) * 64];
+#pragma unroll
+          for (int u = 0; u < 16; ++u) {
+            s0 += (double)bf16_val(w[u] & 0xffffu);
+            s1 += (double)bf16_val(w[u] >> 16);
           }
         }
-        __syncthreads();  // the previous chunk is summed (and the first: nothing reads the area yet)
-#pragma unroll
-        for (int u = 0; u < kQbarStage / (256 * 16); ++u) {
-          const int i = u * 256 + tid;
-          if (i < items) *reinterpret_cast<u32x4_t*>(stage + i * 4) = qv[u];
+        for (; r < jb.bl; ++r) {
+          const uint32_t w = sp[r * 64];
+          s0 += (double)bf16_val(w & 0xffffu);
+          s1 += (double)bf16_val(w >> 16);
         }
-        __syncthreads();
-        if (hs < hp) {
-          // 16 rows' words read together, then added in row order
-          const uint32_t* sp = stage + hs * 64 + l;
-          int r = 0;
-          for (; r + 16 <= n; r += 16) {
-            uint32_t w[16];
+        qs[h * SHD + 2 * l] = (double)bf16_val(f64_to_bf16_bits_2step(s0 / (double)jb.bl));
+        qs[h * SHD + 2 * l + 1] = (double)bf16_val(f64_to_bf16_bits_2step(s1 / (double)jb.bl));
+      }
+    } else {
+      for (int h0 = 0; h0 < g; h0 += 4) {
+        const int hp = min(4, g - h0);             // heads of this pass
+        const int rows_per = kQbarStage / (hp * 256);  // block rows per chunk
+        double s0 = 0.0, s1 = 0.0;
+        for (int t0 = 0; t0 < jb.bl; t0 += rows_per) {
+          const int n = min(rows_per, jb.bl - t0);
+          const int items = n * hp * 16;  // 16-byte pieces of the chunk
+          u32x4_t qv[kQbarStage / (256 * 16)];
 #pragma unroll
-            for (int u = 0; u < 16; ++u) w[u] = sp[(r + u) * hp * 64];
-#pragma unroll
-            for (int u = 0; u < 16; ++u) {
-              s0 += (double)bf16_val(w[u] & 0xffffu);
-              s1 += (double)bf16_val(w[u] >> 16);
+          for (int u = 0; u < kQbarStage / (256 * 16); ++u) {
+            const int i = u * 256 + tid;
+            if (i < items) {
+              const int r = i / (hp * 16), rem = i - r * (hp * 16);
+              qv[u] = ld128(qblk + (int64_t)(t0 + r) * a.q_stride + (h0 + (rem >> 4)) * SHD + (rem & 15) * 8);
             }
           }
-          for (; r < n; ++r) {
-            const uint32_t w = sp[r * hp * 64];
-            s0 += (double)bf16_val(w & 0xffffu);
-            s1 += (double)bf16_val(w >> 16);
+          __syncthreads();  // the previous chunk is summed (and the first: nothing reads the area yet)
+#pragma unroll
+          for (int u = 0; u < kQbarStage / (256 * 16); ++u) {
+            const int i = u * 256 + tid;
+            if (i < items) *reinterpret_cast<u32x4_t*>(stage + i * 4) = qv[u];
+          }
+          __syncthreads();
+          if (hs < hp) {
+            // 16 rows' words read together, then added in row order
+            const uint32_t* sp = stage + hs * 64 + l;
+            int r = 0;
+            for (; r + 16 <= n; r += 16) {
+              uint32_t w[16];
+#pragma unroll
+              for (int u = 0; u < 16; ++u) w[u] = sp[(r + u) * hp * 64];
+#pragma unroll
+              for (int u = 0; u < 16; ++u) {
+                s0 += (double)bf16_val(w[u] & 0xffffu);
+                s1 += (double)bf16_val(w[u] >> 16);
+              }
+            }
+            for (; r < n; ++r) {
+              const uint32_t w = sp[r * hp * 64];
+              s0 += (double)bf16_val(w & 0xffffu);
+              s1 += (double)bf16_val(w >> 16);
+            }
           }
         }
-      }
-      if (hs < hp) {
-        qs[(h0 + hs) * SHD + 2 * l] = (double)bf16_val(f64_to_bf16_bits_2step(s0 / (double)jb.bl));
-        qs[(h0 + hs) * SHD + 2 * l + 1] = (double)bf16_val(f64_to_bf16_bits_2step(s1 / (double)jb.bl));
+        if (hs < hp) {
+          qs[(h0 + hs) * SHD + 2 * l] = (double)bf16_val(f64_to_bf16_bits_2step(s0 / (double)jb.bl));
+          qs[(h0 + hs) * SHD + 2 * l + 1] = (double)bf16_val(f64_to_bf16_bits_2step(s1 / (double)jb.bl));
+        }
       }
     }
     __syncthreads();  // the stage area becomes the K tile

@@ -194,6 +194,9 @@ __device__ __forceinline__ void score_group(const uint8_t* krow, int sw, const d
   }
 }
 
+// G1: the launch has one query head per KV head (a separate instantiation,
+// so that the register allocation of the single-head path is its own).
+template <bool G1>
 __global__ __launch_bounds__(256) void score_kernel(SelArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   uint8_t* kt = lds;
@@ -204,7 +207,7 @@ __global__ __launch_bounds__(256) void score_kernel(SelArgs a) {
   const Job jb = load_job(a, jid);
   const int c0 = blockIdx.x * cpw;
   if (c0 >= jb.kc) return;
-  const int g = a.g;
+  const int g = G1 ? 1 : a.g;
   const int tid = threadIdx.x;
   const int rsub = tid >> 4, ch = tid & 15;
   u32x4_t rows[kScoreCandsMax / 16];
@@ -319,7 +322,7 @@ __global__ __launch_bounds__(256) void score_kernel(SelArgs a) {
     *reinterpret_cast<u32x4_t*>(kt + r * 256 + ((ch ^ (r & 15)) << 4)) = rows[p];
   }
   __syncthreads();
-  if (g == 1) {
+  if constexpr (G1) {
     // thread tid scores candidate tid and, in a workgroup of more than 256,
     // candidate tid + 256: a wavefront with any second candidate runs the two
     // dependent f64 chains interleaved (each still d ascending; lanes without
@@ -390,7 +393,9 @@ __global__ __launch_bounds__(256) void score_kernel(SelArgs a) {
   // chains interleaved (each head still sums d ascending) and every K element
   // converted once for the group; the heads of the group below g are folded
   // into best / part in ascending order
-  if (g > 4) {
+  if (g == 7) {  // Dream-7B's 28 / 4 heads: the exact group, no padded head
+    score_group<7>(krow, sw, qs, 7, best, part);
+  } else if (g > 4) {
     for (int g0 = 0; g0 < g; g0 += 8) score_group<8>(krow, sw, qs + g0 * SHD, min(8, g - g0), best, part);
   } else {
     score_group<4>(krow, sw, qs, g, best, part);
@@ -1044,11 +1049,11 @@ extern "C" int dllm_select_kv_store(const dllm_bf16* q, const dllm_bf16* k, cons
     }
   }
   const size_t score_lds = (size_t)a.score_cpw * 256 + qs_bytes;
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(score_kernel),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)score_lds);
+  auto score = a.g == 1 ? score_kernel<true> : score_kernel<false>;
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(score), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     (int)score_lds);
   if (e != hipSuccess) return fail(DLLM_ERR_HIP, "%s: hipFuncSetAttribute: %s", name, hipGetErrorString(e));
-  score_kernel<<<dim3((unsigned)((max_kc + a.score_cpw - 1) / a.score_cpw), Hkv, n_job), dim3(256), score_lds, st>>>(
-      a);
+  score<<<dim3((unsigned)((max_kc + a.score_cpw - 1) / a.score_cpw), Hkv, n_job), dim3(256), score_lds, st>>>(a);
   int rc = check_launch(name);
   if (rc) return rc;
   // enough top-k workgroups to give every CU one (256 CUs), at most four per (job, KV head)

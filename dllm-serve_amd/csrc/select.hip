@@ -61,6 +61,7 @@ struct SelArgs {
   int64_t* idx_out;  // [n_job][Hkv][max_keep] or null
   int n_part;        // top-k workgroups per (job, KV head): each selects, then copies 1/n_part of the rows
   int score_cpw;     // candidates per score workgroup: a multiple of 16 in [kScoreCands, kScoreCandsMax]
+  int q_dma;         // every q byte lies within 4 GiB of q: 32-bit buffer offsets reach every block row
   // workspace
   uint16_t* raw;     // [n_job][Hkv][max_kc] bf16 bits (head_select jobs)
   double* part;      // [n_job][Hkv][max_kc] per-KV-head sums (token-selection jobs)
@@ -222,7 +223,7 @@ __global__ __launch_bounds__(256) void score_kernel(SelArgs a) {
     uint32_t* stage = reinterpret_cast<uint32_t*>(kt);  // [row][head of the pass][64 words]
     const int hs = tid >> 6, l = tid & 63;
     const uint16_t* qblk = a.q + ((int64_t)jb.row0 + jb.bs) * a.q_stride + (int64_t)kv * g * SHD;
-    if ((g * jb.bl + 3) / 4 * 4 <= cpw) {
+    if (a.q_dma && ((int64_t)g * jb.bl + 3) / 4 * 4 <= cpw) {  // (then g * bl * 16 <= 304 * 16 fits an int)
       // The whole block fits the K-tile area: all its rows arrive at once by
       // buffer DMA, [head][row][16 chunks] (instruction j of wave j % 4 fills
       // 1 KiB = 64 pieces; pieces past the block read as zero), and the heads
@@ -1012,6 +1013,7 @@ extern "C" int dllm_select_kv_store(const dllm_bf16* q, const dllm_bf16* k, cons
   SelArgs a = {};
   a.q = q; a.k = k; a.v = v; a.n_rows = n_rows;
   a.q_stride = q_stride_tok; a.k_stride = k_stride_tok; a.v_stride = v_stride_tok;
+  a.q_dma = n_rows <= ((((int64_t)1 << 32) - 1) / (q_stride_tok * 2)) ? 1 : 0;  // q_stride_tok >= Hq * D > 0 here
   a.jobs = jobs; a.n_job = n_job; a.max_kc = max_kc; a.max_keep = max_keep;
   a.Hq = Hq; a.Hkv = Hkv; a.g = Hq / Hkv;
   a.sqrt_d = sqrt_d;

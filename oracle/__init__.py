@@ -16,6 +16,8 @@ Modules
   rope       NeoX rotary embedding (input preparation; expected results of the K7 kernel)
   sampler    low-confidence remasking: softmax-max of logit rows (with the
              Gumbel transform at temperature > 0) and the unmasking step
+  step       per-step inputs of a batch: sparse state and its advance, rows
+             fed and positions, cu_seqlens_k, slot lists
   configs    seeded synthetic inputs of the benchmark configurations
 
 Parity pins (what checks each function; see tests/test_oracle_*.py):
@@ -32,6 +34,9 @@ Parity pins (what checks each function; see tests/test_oracle_*.py):
              confidences, counting and tie-order invariants; the published
              SplitMix64 outputs, the reference's add_gumbel_noise ops on the
              same draws, Gumbel-max frequencies against softmax
+  step       hand-derived state sequences for delay 0 / 1 / 2 / 5, block
+             spans (including the reference's past-the-end over-count), n_keep
+             and slot-list closed forms on hand-checked cases
 The reference's own tests hold no numeric fixtures for this path, and its
 package cannot be imported here (it needs flash_attn), so no function is
 pinned against reference-produced vectors.

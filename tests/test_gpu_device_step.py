@@ -6,7 +6,9 @@ denoising steps replayed from captured HIP graphs.
   ratios and prompt lengths), the tables the device builds equal the ones the
   host path builds (StepPlan from prepare_step's Context, prepare_step's
   positions, step_windows) and the device state advanced by the kernel
-  equals the host Sequence objects' state, entry for entry.
+  equals the host Sequence objects' state, entry for entry.  The same tables
+  are also checked against oracle.step (rows, positions, cu_seqlens_k, slot
+  lists, selection jobs, cached segments).
 * A tiny model (2 layers, 2 heads x 128, vocabulary 1024) denoises a mixed
   batch eagerly on the host path and again with StepGraphs (device tables,
   steps captured once per launch shape and replayed); the generated tokens
@@ -14,6 +16,8 @@ denoising steps replayed from captured HIP graphs.
 import numpy as np
 import pytest
 import torch
+
+from oracle import step as ostep
 
 from dllm_serve_amd import _capi
 from dllm_serve_amd.engine.device_step import DeviceStepState, StepGraphs, state_row
@@ -44,6 +48,37 @@ def _np(t):
     return t.cpu().numpy()
 
 
+def _mirror(s):
+    st = s.sparse_state
+    cfg = None if st is None else ostep.Cfg(st.config.default_block_len, st.config.retention_ratio,
+                                            st.config.delay_step)
+    return ostep.SparseSeq(s.num_prompt_tokens, s.num_tokens, s.block_table if st is not None else (), cfg)
+
+
+def _check_tables_against_oracle(t, mirrors, step):
+    """Device-built tables of one step against oracle.step."""
+    per, cu = ostep.step_inputs(mirrors)
+    p = t.plan
+    assert list(_np(p.cu)) == list(cu), f"step {step}: cu"
+    assert np.array_equal(_np(t.positions), np.concatenate([q for _, q, _ in per])), f"step {step}: positions"
+    jobs = _np(p.jobs)[:8 * p.n_job].reshape(-1, 8)
+    slots = _np(p.slots)
+    cached = list(_np(p.cached_ids)[:p.n_cached])
+    slot_off = _np(p.slot_off)
+    dense = set(_np(p.dense_ids)[:p.n_dense].tolist())
+    for i, (mode, q, sl) in enumerate(per):
+        assert (i in dense) == (mode in (0, 1)), (step, i)
+        if mode == 1:
+            row = [r for r in jobs if r[0] == cu[i]]
+            assert len(row) == 1, (step, i)
+            bs, bl = mirrors[i].span()
+            assert list(row[0][1:5]) == [len(q), bs, bl, len(sl)], (step, i)
+            assert list(slots[row[0][5]:row[0][5] + len(sl)]) == sl, (step, i)
+        elif mode == 2:
+            r = cached.index(i)
+            assert list(slots[slot_off[r]:slot_off[r + 1]]) == sl, (step, i)
+
+
 def test_device_tables_equal_host_tables(dev):
     cfgs = [None,
             SparseConfig(default_block_len=8, retention_ratio=0.5, delay_step=1, head_select=True),
@@ -55,6 +90,7 @@ def test_device_tables_equal_host_tables(dev):
     seqs, _ = _batch(dev, specs, steps=16)
     N = max(s.num_tokens for s in seqs) + 3
     ds = DeviceStepState(seqs, dev, N)
+    mirrors = [_mirror(s) for s in seqs]
     checked = 0
     for step in range(16):
         print(f"device tables step {step}", flush=True)
@@ -92,10 +128,13 @@ def test_device_tables_equal_host_tables(dev):
                 r += n
             assert np.array_equal(_np(t.smp_params), np.array(want_p, np.int32))
             assert np.array_equal(_np(t.smp_rows), np.array(want_rows, np.int64))
+            _check_tables_against_oracle(t, mirrors, step)
             checked += 1
         ds.advance()
-        for s in seqs:
+        for s, m in zip(seqs, mirrors):
             s.advance()
+            if m.cfg is not None:
+                m.advance()
         torch.cuda.synchronize()
         assert np.array_equal(_np(ds.state), np.array([state_row(s) for s in seqs], np.int32)), f"step {step}"
     assert checked >= 8

@@ -656,6 +656,97 @@ __device__ __forceinline__ void cached_merge_store(const AttnArgs& a, uint8_t* l
 }
 
 
+// The merge of cached_merge_store for one row block per workgroup (RB = 1).
+// Each wavefront reads only its own 32 rows of every tile, so its rows of the
+// stage the last tile did not use are free without a barrier: its unscaled
+// O^T partial goes there as [row][d] f32 (d 0..63 in its K rows, 64..127 in
+// its V rows; 16-byte chunk c of a row at c ^ (row & 15), so that 16 lanes on
+// 16 rows hit 16 different chunks), and its row maxima and sums into its own
+// entries of the idle slot ring.  One barrier, then thread (row q, d0 .. d0 +
+// 15) merges the four partials, wavefronts in order, each scaled term (and
+// each term of the row sum) rounded before it is added.
+__device__ __forceinline__ void cached_merge_store_rb1(const AttnArgs& a, uint8_t* lds, int last_stage,
+                                                       float* ml, const DenseState<1>& st, int s, int hkv, int mt,
+                                                       int split, int qrow0, int M, int m_base, int g, int tid) {
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int lrow = lane & 31;
+  const int hl = lane >> 5;
+  uint8_t* part = lds + (last_stage ^ 1) * CK_STAGE;  // piece p of wave w: part + p * CK_TILE * 256 + w * 8 KiB
+  const float l_tot = pair_sum32(st.l_run[0]);
+  if (hl == 0) {
+    ml[(wave * 2 + 0) * 32 + lrow] = st.m_run[0];
+    ml[(wave * 2 + 1) * 32 + lrow] = l_tot;
+  }
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int rq = 0; rq < 4; ++rq) {
+      const int d = db * 32 + 8 * rq + 4 * hl;
+      uint8_t* row = part + (d >> 6) * CK_TILE * 256 + (wave * 32 + lrow) * 256;
+      const f32x4_t v = {st.oacc[0][db][4 * rq], st.oacc[0][db][4 * rq + 1], st.oacc[0][db][4 * rq + 2],
+                         st.oacc[0][db][4 * rq + 3]};
+      *reinterpret_cast<f32x4_t*>(row + ((((d & 63) >> 2) ^ (lrow & 15)) << 4)) = v;
+    }
+  lds_barrier();
+  const int q = tid & 31;
+  const int d0 = (tid >> 5) * 16;
+  float mw[4], mq = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    mw[w] = ml[(w * 2) * 32 + q];
+    mq = fmaxf(mq, mw[w]);
+  }
+  const float mq_use = (mq == -INFINITY) ? 0.f : mq;
+  float lq = 0.f;
+  float acc[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const float f = (mw[w] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(mw[w] - mq_use);
+    lq = __fadd_rn(lq, __fmul_rn(ml[(w * 2 + 1) * 32 + q], f));  // f = 0 for a wavefront without keys
+    const uint8_t* row = part + (d0 >> 6) * CK_TILE * 256 + (w * 32 + q) * 256;
+#pragma unroll
+    for (int c4 = 0; c4 < 4; ++c4) {
+      const f32x4_t v = *reinterpret_cast<const f32x4_t*>(row + (((((d0 & 63) >> 2) + c4) ^ (q & 15)) << 4));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[4 * c4 + e] = __fadd_rn(acc[4 * c4 + e], __fmul_rn(v[e], f));
+    }
+  }
+  const int mrow = m_base + q;
+  if (mrow < M) {
+    const int tq = mrow / g;
+    const int hq = hkv * g + (mrow - tq * g);
+    if (a.n_split == 1) {
+      const float inv = lq > 0.f ? 1.f / lq : 0.f;
+      uint16_t* op = a.o + (int64_t)(qrow0 + tq) * a.o_stride + hq * HD + d0;
+      u32x4_t w0, w1;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        w0[w] = cvt_pk_bf16(acc[2 * w] * inv, acc[2 * w + 1] * inv);
+        w1[w] = cvt_pk_bf16(acc[8 + 2 * w] * inv, acc[8 + 2 * w + 1] * inv);
+      }
+      st128(op, w0);
+      st128(op + 8, w1);
+    } else {
+      const int64_t Prec = (((int64_t)s * a.Hkv + hkv) * a.mtiles + mt) * a.n_split + split;
+      float* po = a.ws + (Prec * 32 + q) * HD + d0;
+#pragma unroll
+      for (int i = 0; i < 16; i += 4) {
+        f32x4_t v4 = {acc[i], acc[i + 1], acc[i + 2], acc[i + 3]};
+        *reinterpret_cast<f32x4_t*>(po + i) = v4;
+      }
+      if (d0 == 0) {  // one writer per row
+        const int64_t nrec = (int64_t)a.n_seg * a.Hkv * a.mtiles * a.n_split;
+        float* pml = a.ws + nrec * 32 * HD + (Prec * 32 + q) * 2;
+        pml[0] = mq;
+        pml[1] = lq;
+      }
+    }
+  }
+}
+
 // One 32-key block of the four-wavefront K3b: K operands from LDS, keys set in
 // `bad` left out of the softmax by a small conditional block (a single
 // softmax code path keeps the accumulators in place).
@@ -912,7 +1003,11 @@ __global__ __launch_bounds__(256 * RB) __attribute__((amdgpu_waves_per_eu(2, 2))
     bad_t0 = bad_t1;
     bad_t1 = bad_t2;
   }
-  cached_merge_store(a, lds + rblk * CK_MERGE_BYTES, st, s, hkv, mt, split, qrow0, M, m_base, g, tid & 255);
+  if constexpr (RB == 1)
+    cached_merge_store_rb1(a, lds, (ntiles - 1) & 1, reinterpret_cast<float*>(slot_ring), st, s, hkv, mt, split,
+                           qrow0, M, m_base, g, tid);
+  else
+    cached_merge_store(a, lds + rblk * CK_MERGE_BYTES, st, s, hkv, mt, split, qrow0, M, m_base, g, tid & 255);
 }
 
 // Merge the n_split partial records of every (segment, head, M row).

@@ -539,15 +539,9 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(OCC, OC
 // softmax.
 constexpr int CK_TILE = 128;
 constexpr int CK_STAGE = 2 * CK_TILE * 256;
-constexpr int CK_MERGE_LD = 34;
-constexpr int CK_MERGE_BYTES = (8 * 32 + 4 * HD * CK_MERGE_LD) * 4;  // one row block's merge area
-static_assert(CK_MERGE_BYTES <= 2 * CK_STAGE, "a merge area fits in the two stages");
-// LDS of the kernel with RB row blocks: two stages, the slot ring
-// ([4 tiles][4 RB wavefronts][64] words), or RB merge areas if larger
-constexpr int ck_lds_bytes(int rb) {
-  return 2 * CK_STAGE + 4 * 4 * rb * 64 * 4 > rb * CK_MERGE_BYTES ? 2 * CK_STAGE + 4 * 4 * rb * 64 * 4
-                                                                  : rb * CK_MERGE_BYTES;
-}
+// LDS of the kernel with RB row blocks: two stages and the slot ring
+// ([4 tiles][4 RB wavefronts][64] words); the final merge reuses both
+constexpr int ck_lds_bytes(int rb) { return 2 * CK_STAGE + 4 * 4 * rb * 64 * 4; }
 
 // Cache and block rows of a segment are read by exactly one workgroup, each
 // 16-byte piece by one lane of one DMA instruction: streaming loads (the q
@@ -558,137 +552,56 @@ __device__ __forceinline__ void gdma16(const void* g, uint8_t* lds_dst) {
 }
 
 // The four wavefronts' softmax states of one row block (each holds the same
-// 32 M rows over its own keys) merged in LDS at `lds`, normalised and written
-// to o -- or, when the keys are split across workgroups, written as a partial
-// record for attn_combine_kernel.  Every thread of the workgroup calls it
-// once (it holds workgroup barriers); `tid` is the thread's index within its
-// row block's 256 threads.
-__device__ __forceinline__ void cached_merge_store(const AttnArgs& a, uint8_t* lds, const DenseState<1>& st, int s,
-                                                   int hkv, int mt, int split, int qrow0, int M, int m_base, int g,
-                                                   int tid) {
-  const int wave = tid >> 6;
+// 32 M rows over its own keys) merged, normalised and written to o -- or,
+// when the keys are split across workgroups, written as a partial record
+// for attn_combine_kernel.  Every thread of the workgroup calls it once (it
+// holds workgroup barriers).  The four wavefronts of a row block park their
+// unscaled O^T partials as [row][d] f32 in 32 rows x 2 x 256 bytes of a
+// stage (d 0..63 in the K rows, 64..127 in the V rows of their key block;
+// 16-byte chunk c of a row at c ^ (row & 15),
+// so that 16 lanes on 16 rows hit 16 different chunks), and their row maxima
+// and sums in the idle slot ring.  Row block 0 uses the stage the last tile
+// did not use, free once every wavefront has passed the last tile's first
+// barrier (with RB = 1 a wavefront only ever reads its own rows, so at once);
+// row block 1 uses the last tile's stage after one more barrier.  Then thread
+// (row q, d0 .. d0 + 15) of each row block merges its four partials,
+// wavefronts in order, each scaled term (and each term of the row sum)
+// rounded before it is added.
+template <int RB>
+__device__ __forceinline__ void cached_merge_store(const AttnArgs& a, uint8_t* lds, int last_stage, float* ring,
+                                                        const DenseState<1>& st, int s, int hkv, int mt, int split,
+                                                        int qrow0, int M, int m_base, int g, int tid, int rblk) {
+  const int wave = (tid >> 6) & 3;
   const int lane = tid & 63;
   const int lrow = lane & 31;
   const int hl = lane >> 5;
-  __syncthreads();
-
-  // ---- merge the four wavefronts' states (each holds 32 M rows x its keys)
-  // ored rows (one per (wavefront, d)) are kMergeLd floats apart: the read
-  // below has lanes 0..31 on rows q = 0..31 of one d and lanes 32..63 on
-  // d + 16, i.e. 16 * kMergeLd floats further, which puts the two halves on
-  // disjoint banks (a 32-float pitch would put all of them on the same ones).
-  constexpr int kMergeLd = CK_MERGE_LD;
-  const float m_run = st.m_run[0];
-  const float l_tot = pair_sum32(st.l_run[0]);
-  float* red = reinterpret_cast<float*>(lds);
-  float* red_m = red;             // [4][32]
-  float* red_l = red + 4 * 32;    // [4][32]
-  float* ored = red + 8 * 32;     // [4][128][kMergeLd]
-  if (hl == 0) {
-    red_m[wave * 32 + lrow] = m_run;
-    red_l[wave * 32 + lrow] = l_tot;
-  }
-  __syncthreads();
-  float m_all = -INFINITY;
-#pragma unroll
-  for (int w = 0; w < 4; ++w) m_all = fmaxf(m_all, red_m[w * 32 + lrow]);
-  const float m_all_use = (m_all == -INFINITY) ? 0.f : m_all;
-  const float fac = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run - m_all_use);
-#pragma unroll
-  for (int db = 0; db < 4; ++db)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int d = db * 32 + 8 * (i >> 2) + 4 * hl + (i & 3);
-      ored[(wave * HD + d) * kMergeLd + lrow] = st.oacc[0][db][i] * fac;
-    }
-  __syncthreads();
-  const int q = tid & 31;
-  const int d0 = (tid >> 5) * 16;
-  float mq = -INFINITY;
-#pragma unroll
-  for (int w = 0; w < 4; ++w) mq = fmaxf(mq, red_m[w * 32 + q]);
-  const float mq_use = (mq == -INFINITY) ? 0.f : mq;
-  float lq = 0.f;
-#pragma unroll
-  for (int w = 0; w < 4; ++w) {
-    const float mw = red_m[w * 32 + q];
-    lq += (mw == -INFINITY) ? 0.f : red_l[w * 32 + q] * __builtin_amdgcn_exp2f(mw - mq_use);
-  }
-  float acc[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    float sum = 0.f;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) sum += ored[(w * HD + d0 + i) * kMergeLd + q];
-    acc[i] = sum;
-  }
-  const int mrow = m_base + q;
-  if (mrow < M) {
-    const int tq = mrow / g;
-    const int hq = hkv * g + (mrow - tq * g);
-    if (a.n_split == 1) {
-      const float inv = lq > 0.f ? 1.f / lq : 0.f;
-      uint16_t* op = a.o + (int64_t)(qrow0 + tq) * a.o_stride + hq * HD + d0;
-      u32x4_t w0, w1;
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        w0[w] = cvt_pk_bf16(acc[2 * w] * inv, acc[2 * w + 1] * inv);
-        w1[w] = cvt_pk_bf16(acc[8 + 2 * w] * inv, acc[8 + 2 * w + 1] * inv);
-      }
-      st128(op, w0);
-      st128(op + 8, w1);
-    } else {
-      const int64_t Prec = (((int64_t)s * a.Hkv + hkv) * a.mtiles + mt) * a.n_split + split;
-      float* po = a.ws + (Prec * 32 + q) * HD + d0;
-#pragma unroll
-      for (int i = 0; i < 16; i += 4) {
-        f32x4_t v4 = {acc[i], acc[i + 1], acc[i + 2], acc[i + 3]};
-        *reinterpret_cast<f32x4_t*>(po + i) = v4;
-      }
-      if (d0 == 0) {  // one writer per row
-        const int64_t nrec = (int64_t)a.n_seg * a.Hkv * a.mtiles * a.n_split;
-        float* pml = a.ws + nrec * 32 * HD + (Prec * 32 + q) * 2;
-        pml[0] = mq;
-        pml[1] = lq;
-      }
-    }
-  }
-}
-
-
-// The merge of cached_merge_store for one row block per workgroup (RB = 1).
-// Each wavefront reads only its own 32 rows of every tile, so its rows of the
-// stage the last tile did not use are free without a barrier: its unscaled
-// O^T partial goes there as [row][d] f32 (d 0..63 in its K rows, 64..127 in
-// its V rows; 16-byte chunk c of a row at c ^ (row & 15), so that 16 lanes on
-// 16 rows hit 16 different chunks), and its row maxima and sums into its own
-// entries of the idle slot ring.  One barrier, then thread (row q, d0 .. d0 +
-// 15) merges the four partials, wavefronts in order, each scaled term (and
-// each term of the row sum) rounded before it is added.
-__device__ __forceinline__ void cached_merge_store_rb1(const AttnArgs& a, uint8_t* lds, int last_stage,
-                                                       float* ml, const DenseState<1>& st, int s, int hkv, int mt,
-                                                       int split, int qrow0, int M, int m_base, int g, int tid) {
-  const int wave = tid >> 6;
-  const int lane = tid & 63;
-  const int lrow = lane & 31;
-  const int hl = lane >> 5;
-  uint8_t* part = lds + (last_stage ^ 1) * CK_STAGE;  // piece p of wave w: part + p * CK_TILE * 256 + w * 8 KiB
+  // piece p of wave w: part + p * CK_TILE * 256 + w * 8 KiB
+  uint8_t* part = lds + (rblk == 0 ? last_stage ^ 1 : last_stage) * CK_STAGE;
+  float* ml = ring + rblk * 4 * 2 * 32;
   const float l_tot = pair_sum32(st.l_run[0]);
   if (hl == 0) {
     ml[(wave * 2 + 0) * 32 + lrow] = st.m_run[0];
     ml[(wave * 2 + 1) * 32 + lrow] = l_tot;
   }
+  auto park = [&]() {
 #pragma unroll
-  for (int db = 0; db < 4; ++db)
+    for (int db = 0; db < 4; ++db)
 #pragma unroll
-    for (int rq = 0; rq < 4; ++rq) {
-      const int d = db * 32 + 8 * rq + 4 * hl;
-      uint8_t* row = part + (d >> 6) * CK_TILE * 256 + (wave * 32 + lrow) * 256;
-      const f32x4_t v = {st.oacc[0][db][4 * rq], st.oacc[0][db][4 * rq + 1], st.oacc[0][db][4 * rq + 2],
-                         st.oacc[0][db][4 * rq + 3]};
-      *reinterpret_cast<f32x4_t*>(row + ((((d & 63) >> 2) ^ (lrow & 15)) << 4)) = v;
-    }
+      for (int rq = 0; rq < 4; ++rq) {
+        const int d = db * 32 + 8 * rq + 4 * hl;
+        uint8_t* row = part + (d >> 6) * CK_TILE * 256 + (wave * 32 + lrow) * 256;
+        const f32x4_t v = {st.oacc[0][db][4 * rq], st.oacc[0][db][4 * rq + 1], st.oacc[0][db][4 * rq + 2],
+                           st.oacc[0][db][4 * rq + 3]};
+        *reinterpret_cast<f32x4_t*>(row + ((((d & 63) >> 2) ^ (lrow & 15)) << 4)) = v;
+      }
+  };
+  if (rblk == 0) park();
+  if constexpr (RB > 1) {
+    lds_barrier();  // every wavefront is done with the last tile's stage
+    if (rblk == 1) park();
+  }
   lds_barrier();
+  tid &= 255;
   const int q = tid & 31;
   const int d0 = (tid >> 5) * 16;
   float mw[4], mq = -INFINITY;
@@ -1003,11 +916,8 @@ __global__ __launch_bounds__(256 * RB) __attribute__((amdgpu_waves_per_eu(2, 2))
     bad_t0 = bad_t1;
     bad_t1 = bad_t2;
   }
-  if constexpr (RB == 1)
-    cached_merge_store_rb1(a, lds, (ntiles - 1) & 1, reinterpret_cast<float*>(slot_ring), st, s, hkv, mt, split,
-                           qrow0, M, m_base, g, tid);
-  else
-    cached_merge_store(a, lds + rblk * CK_MERGE_BYTES, st, s, hkv, mt, split, qrow0, M, m_base, g, tid & 255);
+  cached_merge_store<RB>(a, lds, (ntiles - 1) & 1, reinterpret_cast<float*>(slot_ring), st, s, hkv, mt, split,
+                              qrow0, M, m_base, g, tid, rblk);
 }
 
 // Merge the n_split partial records of every (segment, head, M row).

@@ -480,11 +480,19 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(OCC, OC
     // The wave's 32 rows x 256 bytes land in its own 8 KiB of the (now free)
     // K/V stages, chunks XOR-swizzled by row; read back, instruction j
     // carries rows 4j .. 4j+3, one 16-byte chunk per lane.
-    // O staging needs NW * 8 KiB at the front of LDS; the launch gives at least that
+    // O staging needs NW * 8 KiB (the Q rows, or the front of LDS); the launch gives at least that
     const float l_tot = pair_sum32(st.l_run[0]);
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-    __syncthreads();  // every wavefront is done reading the K/V stages
-    uint8_t* ot = lds + wave * 8192;
+    // With Q by DMA a wavefront stages O in its own Q rows, which no other
+    // wavefront reads, so it stores as soon as it is done; otherwise in the
+    // K/V stages once every wavefront is done reading them.
+    uint8_t* ot;
+    if constexpr (QDMA) {
+      ot = lds + QOFF + wave * 8192;
+    } else {
+      __syncthreads();
+      ot = lds + wave * 8192;
+    }
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
@@ -1071,7 +1079,7 @@ extern "C" int dllm_attn_varlen_fwd(const dllm_bf16* q, const dllm_bf16* k, cons
                    : (one_wg ? attn_dense_kernel<12, 1, DENSE_ST, 32, 3> : attn_dense_kernel<4, 1, DENSE_ST, 32, 3>);
   int lds_bytes = DENSE_ST * 2 * (wide ? 64 : 32) * 256;
   if (wide || one_wg)
-    lds_bytes += nw * 8192;  // Q rows after the stages (one workgroup per CU); O staging reuses the front
+    lds_bytes += nw * 8192;  // Q rows after the stages (one workgroup per CU), later each wavefront's O staging
   else if (nw * 8192 > lds_bytes)
     lds_bytes = nw * 8192;  // O staging
   if ((rc = set_lds(kern, lds_bytes, name))) return rc;

@@ -49,6 +49,8 @@ def test_c1_single_layer(dev):
     ([300, 384, 1, 257, 383], 32, 32),               # 257..384 M rows, 160 pairs: one 12-wavefront workgroup each
     ([64, 96, 7, 90] * 10, 16, 4),                     # the same launch with GQA (96 x 4 = 384 M rows, 160 pairs)
     ([300, 384, 1, 257, 383], 16, 16),               # the same rows, 80 pairs: three 4-wavefront workgroups each
+    ([500, 33, 1], 32, 1),                             # MQA, g = 32: one KV row serves 32 M rows
+    ([260, 7], 64, 1),                                 # g = 64
 ])
 def test_varlen_ragged(dev, lens, Hq, Hkv):
     print(f"varlen lens={lens} Hq={Hq} Hkv={Hkv}", flush=True)
@@ -182,6 +184,8 @@ def _cached_case(prefix, blk, Hq, Hkv, seed, page=256, extra_pages=3):
     ([0, 1], [8, 3], 8, 8),                                # empty / single cached row
     ([2100 + 13 * i for i in range(32)], [32] * 32, 8, 8),  # 256 pairs: one workgroup per pair, no split
     ([700] * 16, [32] * 16, 28, 4),                        # Dream denoise step: 448 M tiles, paired row blocks
+    ([300, 1000, 0], [32, 16, 5], 32, 1),                  # MQA, g = 32: 32 M tiles per segment, paired row blocks
+    ([257, 40], [3, 9], 64, 1),                            # g = 64, blocks of a few rows
 ])
 def test_block_cached(dev, prefix, blk, Hq, Hkv):
     print(f"block_cached prefix={prefix} blk={blk} Hq={Hq} Hkv={Hkv}", flush=True)

@@ -129,7 +129,7 @@ def store_kvcache(key, value, k_cache, v_cache, slot_mapping, n_tok, row_elems):
     lib = load()
     rc = lib.dllm_store_kvcache(
         key.data_ptr(), key.stride(0), value.data_ptr(), value.stride(0),
-        k_cache.data_ptr(), v_cache.data_ptr(), k_cache.numel() // row_elems,
+        k_cache.data_ptr(), v_cache.data_ptr(), min(k_cache.numel(), v_cache.numel()) // row_elems,
         slot_mapping.data_ptr(), n_tok, row_elems, _stream(key.device))
     _check(rc, "dllm_store_kvcache")
 
@@ -140,7 +140,7 @@ def load_kvcache(key, value, k_cache, v_cache, slot_mapping, n_tok, row_elems):
     lib = load()
     rc = lib.dllm_load_kvcache(
         key.data_ptr(), key.stride(0), value.data_ptr(), value.stride(0),
-        k_cache.data_ptr(), v_cache.data_ptr(), k_cache.numel() // row_elems,
+        k_cache.data_ptr(), v_cache.data_ptr(), min(k_cache.numel(), v_cache.numel()) // row_elems,
         slot_mapping.data_ptr(), n_tok, row_elems, _stream(key.device))
     _check(rc, "dllm_load_kvcache")
 
@@ -195,7 +195,8 @@ def attn_block_cached_fwd(q, k, v, o, cu, seg_ids, n_seg, max_q, max_keys,
     _require_gpu(q, k, v, o, cu, slot_off)
     lib = load()
     Hkv, D = k.shape[1], k.shape[2]
-    cache_slots = k_cache.numel() // (Hkv * D) if k_cache is not None and k_cache.numel() else 0
+    cache_slots = (min(k_cache.numel(), v_cache.numel()) // (Hkv * D)
+                   if k_cache is not None and v_cache is not None and k_cache.numel() else 0)
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
     rc = lib.dllm_attn_block_cached_fwd(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
@@ -219,7 +220,8 @@ def attn_block_cached_fwd_noalloc(q, k, v, o, cu, seg_ids, n_seg, max_q, max_key
     _require_gpu(q, k, v, o, cu, slot_off)
     lib = load()
     Hkv, D = k.shape[1], k.shape[2]
-    cache_slots = k_cache.numel() // (Hkv * D) if k_cache is not None and k_cache.numel() else 0
+    cache_slots = (min(k_cache.numel(), v_cache.numel()) // (Hkv * D)
+                   if k_cache is not None and v_cache is not None and k_cache.numel() else 0)
     rc = lib.dllm_attn_block_cached_fwd_noalloc(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
         cu.data_ptr(), _ptr(seg_ids), n_seg, max_q, max_keys,
@@ -248,7 +250,7 @@ def select_kv_store(q, k, v, jobs, n_job, max_kc, max_keep, sqrt_d, k_cache, v_c
         q.data_ptr(), k.data_ptr(), v.data_ptr(), min(q.shape[0], k.shape[0], v.shape[0]),
         q.stride(0), k.stride(0), v.stride(0),
         jobs.data_ptr(), n_job, max_kc, max_keep, Hq, Hkv, D, float(sqrt_d),
-        k_cache.data_ptr(), v_cache.data_ptr(), k_cache.numel() // (Hkv * D),
+        k_cache.data_ptr(), v_cache.data_ptr(), min(k_cache.numel(), v_cache.numel()) // (Hkv * D),
         slots.data_ptr(), slots.numel(), _ptr(idx_out), _ptr(workspace), ws_bytes, _stream(q.device))
     _check(rc, "dllm_select_kv_store")
 

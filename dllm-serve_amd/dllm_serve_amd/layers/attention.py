@@ -23,6 +23,7 @@ current HIP stream; nothing falls back to the CPU.
 from __future__ import annotations
 
 import os
+import weakref
 
 import numpy as np
 import torch
@@ -254,7 +255,11 @@ class StepPlan:
         self.slot_off, self.jobs, self.slots = slot_off, jobs, slots
         return self
 
-    def workspace(self, key: str, nbytes: int) -> torch.Tensor | None:
+    def workspace(self, key, nbytes: int) -> torch.Tensor | None:
+        """A device buffer of at least ``nbytes`` kept under ``key`` for the
+        step.  A larger request under the same key replaces (and frees) the
+        earlier buffer, so a caller that keeps an address must key by
+        everything the size depends on."""
         if nbytes <= 0:
             return None
         t = self._ws.get(key)
@@ -265,16 +270,20 @@ class StepPlan:
 
     def launch_args(self, Hq: int, Hkv: int, D: int) -> dict:
         """Device addresses of the step's tables and the K3b workspace for
-        one head shape, computed once per step for all layers."""
+        one head shape, computed once per step for all layers.  The workspace
+        is keyed by the head shape and held in the returned dict, so the
+        address cached here stays valid while the plan lives, whatever other
+        head shapes later ask for."""
         key = (Hq, Hkv, D)
         a = self._args.get(key)
         if a is None:
-            ws = self.workspace("cached", _capi.block_cached_workspace_size(
+            ws = self.workspace(("cached",) + key, _capi.block_cached_workspace_size(
                 self.n_cached, self.max_q_cached, self.max_keys_cached, Hq, Hkv, D)) if self.n_cached else None
             a = dict(cu=self.cu.data_ptr(), slots=self.slots.data_ptr(), slot_off=self.slot_off.data_ptr(),
                      dense_ids=None if self.dense_identity else self.dense_ids.data_ptr(),
                      cached_ids=None if self.cached_identity else self.cached_ids.data_ptr(),
-                     ws=None if ws is None else ws.data_ptr(), ws_bytes=0 if ws is None else ws.numel())
+                     ws=None if ws is None else ws.data_ptr(), ws_bytes=0 if ws is None else ws.numel(),
+                     ws_tensor=ws)
             self._args[key] = a
         return a
 
@@ -294,7 +303,10 @@ class Attention(nn.Module):
         self.k_cache = self.v_cache = torch.tensor([])
         self.layer_id = None
         self.last_select_indices = None
-        self._cache_ok = None  # (tensors, addresses, sizes) of the last bound cache that passed _check_cache
+        # (weak references, addresses, sizes, device, result) of the last bound
+        # cache that passed _check_cache: weak, so that a cache the runner
+        # drops or re-sizes is freed at once, not kept alive by this check
+        self._cache_ok = None
 
     def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
         # q/k/v as [rows, heads * head_dim] or [rows, heads, head_dim] are used
@@ -321,9 +333,9 @@ class Attention(nn.Module):
         cache that passed keeps passing while the same tensors keep their
         addresses and sizes."""
         kc, vc = self.k_cache, self.v_cache
-        key = (kc, vc, kc.data_ptr(), vc.data_ptr(), kc.numel(), vc.numel(), device)
+        key = (kc.data_ptr(), vc.data_ptr(), kc.numel(), vc.numel(), device)
         ok = self._cache_ok
-        if ok is not None and ok[0] is kc and ok[1] is vc and ok[2:7] == key[2:]:
+        if ok is not None and ok[0]() is kc and ok[1]() is vc and ok[2:7] == key:
             return ok[7]
         for t, n in ((kc, "k_cache"), (vc, "v_cache")):
             if (t.dtype != torch.bfloat16 or not t.is_contiguous() or t.device != device or t.dim() < 2
@@ -331,7 +343,7 @@ class Attention(nn.Module):
                 raise ValueError(f"{n} must be a contiguous bf16 tensor [..., {self.num_kv_heads}, {self.head_dim}] "
                                  f"on {device}; got {t.dtype} {tuple(t.shape)} on {t.device}")
         res = (kc.data_ptr(), vc.data_ptr(), min(kc.numel(), vc.numel()) // (self.num_kv_heads * self.head_dim))
-        self._cache_ok = key + (res,)
+        self._cache_ok = (weakref.ref(kc), weakref.ref(vc)) + key + (res,)
         return res
 
     def _mixed_sparse_dense_attention(self, q, k, v, context):

@@ -93,3 +93,81 @@ def test_rebound_cache_is_checked_again(dev):
         torch.cuda.synchronize()
     finally:
         reset_context()
+
+
+def test_layers_of_two_head_shapes_share_one_step(dev):
+    """Two Attention layers of different head shapes in one context, the
+    smaller first.  Each layer's K3b launch splits its keys and so needs the
+    step's partial-record workspace; the larger shape asks for more bytes.
+    The smaller layer's workspace must stay its own when the larger one
+    allocates: buffers of the smaller workspace's size allocated in between
+    (the caching allocator hands freed blocks out again) keep their sentinel
+    through the smaller layer's next call, and every output matches the
+    oracle, over two reuse steps."""
+    import numpy as np
+
+    from helpers import assert_attn_close, to_np
+    from oracle import attention as oatt
+    from dllm_serve_amd.engine.sequence import slot_mapping_for
+
+    print("layer host path: two head shapes in one step", flush=True)
+    D = 128
+    shapes = [(8, 2), (32, 8)]  # (Hq, Hkv), the smaller workspace first
+    n_pages = 16
+    gen = torch.Generator().manual_seed(21)
+    layers, caches = [], []
+    for Hq, Hkv in shapes:
+        attn = Attention(Hq, D, D ** -0.5, Hkv, causal=False)
+        cache = torch.randn(2, n_pages, 256, Hkv, D, generator=gen).to(torch.bfloat16).to(dev)
+        attn.k_cache, attn.v_cache = cache[0], cache[1]
+        layers.append(attn)
+        caches.append(cache)
+    cfg = SparseConfig(enabled=True, default_block_len=32, retention_ratio=0.5, pool_kernel=3, delay_step=1,
+                       head_select=True)
+    seqs = [Sequence([2] * 2000, 64, MASK, cfg, device=dev), Sequence([3] * 1800, 64, MASK, cfg, device=dev)]
+    alloc = PageAllocator(range(n_pages))
+    for s in seqs:
+        alloc.allocate(s)
+    try:
+        for _ in range(2):  # steps 0 and 1 only advance the state machine here
+            prepare_step(seqs, dev)
+            reset_context()
+            for s in seqs:
+                s.advance()
+        slot_lists = [slot_mapping_for(s) for s in seqs]
+        assert [len(x) for x in slot_lists] == [1016, 916]
+        for step in range(2):
+            prepare_step(seqs, dev)
+            n = 64
+            ins = []
+            for Hq, Hkv in shapes:
+                q = torch.randn(n, Hq, D, generator=gen).to(torch.bfloat16)
+                k = torch.randn(n, Hkv, D, generator=gen).to(torch.bfloat16)
+                v = torch.randn(n, Hkv, D, generator=gen).to(torch.bfloat16)
+                ins.append((q, k, v, q.to(dev), k.to(dev), v.to(dev)))
+            plan = get_context()._dllm_plan
+            ws_small = _capi.block_cached_workspace_size(2, 32, 32 + 1016, 8, 2, D)
+            ws_large = _capi.block_cached_workspace_size(2, 32, 32 + 1016, 32, 8, D)
+            assert 0 < ws_small < ws_large, (ws_small, ws_large)
+            outs = [layers[0](*ins[0][3:]), layers[1](*ins[1][3:])]
+            sentinels = [torch.full((ws_small,), 0x5A, dtype=torch.uint8, device=dev) for _ in range(4)]
+            outs.append(layers[0](*ins[0][3:]))
+            torch.cuda.synchronize()
+            for t in sentinels:
+                assert bool((t == 0x5A).all()), "a freed workspace was written after the allocator handed it out"
+            assert plan.launch_args(8, 2, D)["ws_tensor"] is not None
+            for li, out in zip((0, 1, 0), outs):
+                Hq, Hkv = shapes[li]
+                q, k, v = ins[li][:3]
+                kc = to_np(caches[li][0]).reshape(-1, Hkv, D)
+                vc = to_np(caches[li][1]).reshape(-1, Hkv, D)
+                ref = np.concatenate([
+                    oatt.block_cached(to_np(q[32 * i:32 * i + 32]), to_np(k[32 * i:32 * i + 32]),
+                                      to_np(v[32 * i:32 * i + 32]), kc, vc, slot_lists[i], D ** -0.5,
+                                      dtype=np.float32) for i in range(2)])
+                assert_attn_close(out.view(n, Hq, D), ref, f"step {step} layer shape {shapes[li]}")
+            reset_context()
+            for s in seqs:
+                s.advance()
+    finally:
+        reset_context()

@@ -113,14 +113,16 @@ __device__ __forceinline__ u32x2_t ds_read_tr16(const uint8_t* p) {
 // A DMA instruction q writes tile rows R = 4q + L/16 (L = lane), physical
 // chunk P = L % 16, i.e. global chunk P ^ (R & 15) (K) or P ^ 4(R & 3) (V):
 //   K: (L/16)*kS + ((P ^ (L/16)) * 16 ^ 64 (q & 3))      V: (L/16)*vS + (P ^ 4(L/16))*16
+// (the XOR acts on the chunk offset alone, the row offset is added after it)
 struct DenseAddr {
   uint32_t kbase, vbase;
-  uint32_t kdma, vdma;
+  uint32_t kdma_row, kdma_chunk, vdma;
 };
 
 __device__ __forceinline__ void dense_addr(DenseAddr& ad, int lane, uint32_t kS, uint32_t vS) {
   const int rl = lane >> 4, P = lane & 15;
-  ad.kdma = (uint32_t)rl * kS + (uint32_t)((P ^ rl) * 16);
+  ad.kdma_row = (uint32_t)rl * kS;
+  ad.kdma_chunk = (uint32_t)((P ^ rl) * 16);
   ad.vdma = (uint32_t)rl * vS + (uint32_t)((P ^ (4 * rl)) * 16);
   const int lrow = lane & 31, hl = lane >> 5;
   ad.kbase = (uint32_t)(lrow * 256 + ((hl ^ (lrow & 15)) * 16));
@@ -378,7 +380,10 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(OCC, OC
       const int q = NW > NDMA ? wave : DMA_PER_WAVE * wave + j;
       if (q >= NDMA) break;  // wave-uniform
       const uint32_t row = (uint32_t)(4 * q);
-      dma16<KV_AUX>(krs, stage + q * 1024, row * kS + (ad.kdma ^ (uint32_t)(64 * (q & 3))));
+      // the swizzle XOR applies to the chunk only: with a token stride that
+      // is not a multiple of 256 bytes, XOR-ing rl * kS + chunk would carry
+      // into the row offset
+      dma16<KV_AUX>(krs, stage + q * 1024, row * kS + ad.kdma_row + (ad.kdma_chunk ^ (uint32_t)(64 * (q & 3))));
       dma16<KV_AUX>(vrs, stage + TK * 256 + q * 1024, row * vS + ad.vdma);
     }
   };
@@ -1027,6 +1032,49 @@ static int set_lds(KernelFn fn, int bytes, const char* name) {
 
 using namespace dllm;
 
+// K3a launch shape: wavefronts per workgroup (4, 12 or 8), keys per tile,
+// M tiles per (segment, KV head), XCD chunk and grid.  One function for the
+// launch and for dllm_attn_varlen_launch_shape, so that the two cannot drift.
+struct DensePlan {
+  int nw, tk, mtiles, xcd_chunk, grid;
+  int64_t logical;
+};
+static DensePlan dense_plan(int n_seg, int max_seqlen_q, int max_seqlen_k, int Hq, int Hkv) {
+  DensePlan p = {};
+  const int g = Hq / Hkv;
+  const bool wide = max_seqlen_k >= DENSE_LONG_K;
+  // (segment, KV head) pairs of 257..384 M rows: one 12-wavefront workgroup
+  // each, so the pair's K/V tiles are read into LDS once instead of by three
+  // workgroups (3 % faster for 8 x 384 tokens, 32 heads) -- when there are
+  // enough pairs to occupy most of the 256 CUs.  Fewer pairs run faster as
+  // three 4-wavefront workgroups each (32 heads x 384 tokens: 1 sequence
+  // 12.6 vs 19.8 us, 4 sequences 20.2 vs 23.3 us; 6 sequences 27.4 vs 25.1).
+  const int64_t m_rows = (int64_t)max_seqlen_q * g;
+  const bool one_wg = !wide && m_rows > 256 && m_rows <= 384 && (int64_t)n_seg * Hkv >= kOneWgMinPairs;
+  p.nw = wide ? 8 : (one_wg ? 12 : 4);
+  p.tk = wide ? 64 : 32;
+  const int bm = 32 * p.nw;
+  p.mtiles = (int)((m_rows + bm - 1) / bm);
+  p.logical = (int64_t)p.mtiles * Hkv * n_seg;
+  // chunks of up to 16 m-tiles of one (segment, KV head): 4..16 measured
+  // within 2 % of one contiguous range per XCD on uniform batches
+  p.xcd_chunk = p.mtiles < 16 ? p.mtiles : 16;
+  const int64_t grain = 8 * (int64_t)p.xcd_chunk;
+  p.grid = (int)((p.logical + grain - 1) / grain * grain);
+  return p;
+}
+
+extern "C" int dllm_attn_varlen_launch_shape(int n_seg, int max_seqlen_q, int max_seqlen_k, int Hq, int Hkv, int D,
+                                             int* wavefronts, int* tile_keys, int* grid) {
+  if (D != HD || Hq <= 0 || Hkv <= 0 || Hq % Hkv || n_seg < 0 || max_seqlen_q < 0 || max_seqlen_k < 0)
+    return fail(DLLM_ERR_INVALID_ARG, "dllm_attn_varlen_launch_shape: unsupported sizes");
+  const DensePlan p = dense_plan(n_seg, max_seqlen_q, max_seqlen_k, Hq, Hkv);
+  if (wavefronts) *wavefronts = p.nw;
+  if (tile_keys) *tile_keys = p.tk;
+  if (grid) *grid = (n_seg == 0 || max_seqlen_q == 0) ? 0 : p.grid;
+  return DLLM_OK;
+}
+
 extern "C" int dllm_attn_varlen_fwd(const dllm_bf16* q, const dllm_bf16* k, const dllm_bf16* v, dllm_bf16* o,
                                     const int32_t* cu_q, const int32_t* cu_k, const int32_t* seg_ids, int n_seg,
                                     int max_seqlen_q, int max_seqlen_k, int Hq, int Hkv, int D, int64_t q_stride_tok,
@@ -1051,22 +1099,13 @@ extern "C" int dllm_attn_varlen_fwd(const dllm_bf16* q, const dllm_bf16* k, cons
   a.cu_q = cu_q; a.cu_k = cu_k; a.seg_ids = seg_ids;
   a.q_stride = q_stride_tok; a.k_stride = k_stride_tok; a.v_stride = v_stride_tok; a.o_stride = o_stride_tok;
   a.n_seg = n_seg; a.Hkv = Hkv; a.g = Hq / Hkv;
-  const bool wide = max_seqlen_k >= DENSE_LONG_K;
-  // (segment, KV head) pairs of 257..384 M rows: one 12-wavefront workgroup
-  // each, so the pair's K/V tiles are read into LDS once instead of by three
-  // workgroups (3 % faster for 8 x 384 tokens, 32 heads) -- when there are
-  // enough pairs to occupy most of the 256 CUs.  Fewer pairs run faster as
-  // three 4-wavefront workgroups each (32 heads x 384 tokens: 1 sequence
-  // 12.6 vs 19.8 us, 4 sequences 20.2 vs 23.3 us; 6 sequences 27.4 vs 25.1).
-  const int64_t m_rows = (int64_t)max_seqlen_q * (Hq / Hkv);
-  const bool one_wg = !wide && m_rows > 256 && m_rows <= 384 && (int64_t)n_seg * Hkv >= kOneWgMinPairs;
-  const int nw = wide ? 8 : (one_wg ? 12 : 4);
-  const int bm = 32 * nw;
-  a.mtiles = (int)(((int64_t)max_seqlen_q * a.g + bm - 1) / bm);
+  const DensePlan plan = dense_plan(n_seg, max_seqlen_q, max_seqlen_k, Hq, Hkv);
+  const bool wide = plan.nw == 8, one_wg = plan.nw == 12;
+  const int nw = plan.nw;
+  a.mtiles = plan.mtiles;
   a.n_split = 1;
-  const int64_t logical = (int64_t)a.mtiles * Hkv * n_seg;
-  if (logical > (int64_t)1 << 30) return fail(DLLM_ERR_INVALID_ARG, "%s: problem too large", name);
-  a.logical_blocks = (int)logical;
+  if (plan.logical > (int64_t)1 << 30) return fail(DLLM_ERR_INVALID_ARG, "%s: problem too large", name);
+  a.logical_blocks = (int)plan.logical;
   a.scale_log2 = softmax_scale * kLog2e;
   // Long key streams: 8 wavefronts (256 M rows) per workgroup, 64-key tiles,
   // one workgroup per CU.  Shorter ones: 4 wavefronts, 32-key tiles, three
@@ -1083,12 +1122,8 @@ extern "C" int dllm_attn_varlen_fwd(const dllm_bf16* q, const dllm_bf16* k, cons
   else if (nw * 8192 > lds_bytes)
     lds_bytes = nw * 8192;  // O staging
   if ((rc = set_lds(kern, lds_bytes, name))) return rc;
-  // chunks of up to 16 m-tiles of one (segment, KV head): 4..16 measured
-  // within 2 % of one contiguous range per XCD on uniform batches
-  a.xcd_chunk = a.mtiles < 16 ? a.mtiles : 16;
-  const int64_t grain = 8 * (int64_t)a.xcd_chunk;
-  const int nb = (int)((logical + grain - 1) / grain * grain);
-  kern<<<dim3(nb), dim3(64 * nw), lds_bytes, reinterpret_cast<hipStream_t>(stream)>>>(a);
+  a.xcd_chunk = plan.xcd_chunk;
+  kern<<<dim3(plan.grid), dim3(64 * nw), lds_bytes, reinterpret_cast<hipStream_t>(stream)>>>(a);
   return check_launch(name);
 }
 
@@ -1131,6 +1166,22 @@ extern "C" size_t dllm_attn_block_cached_workspace_size(int n_seg, int max_q, in
   if (n_split <= 1) return 0;
   const size_t nrec = (size_t)n_seg * Hkv * mtiles * n_split;
   return nrec * 32 * (HD + 2) * sizeof(float);
+}
+
+extern "C" int dllm_attn_block_cached_launch_shape(int n_seg, int max_q, int max_keys, int Hq, int Hkv, int D,
+                                                   int* row_blocks, int* n_split, int* grid) {
+  if (D != HD || Hq <= 0 || Hkv <= 0 || Hq % Hkv || n_seg < 0 || max_q < 0 || max_keys < 0)
+    return fail(DLLM_ERR_INVALID_ARG, "dllm_attn_block_cached_launch_shape: unsupported sizes");
+  int mtiles = 0, rb = 1, ns = 1, kps = 0;
+  block_cached_plan(n_seg, max_q, max_keys, Hq, Hkv, mtiles, rb, ns, kps);
+  const int mblocks = (mtiles + rb - 1) / rb;
+  const int64_t logical = (int64_t)ns * mblocks * Hkv * n_seg;
+  const int64_t per_pair = (int64_t)ns * mblocks;
+  const int64_t grain = 8 * (per_pair < 16 ? per_pair : 16);
+  if (row_blocks) *row_blocks = rb;
+  if (n_split) *n_split = ns;
+  if (grid) *grid = (n_seg == 0 || max_q == 0) ? 0 : (int)((logical + grain - 1) / grain * grain);
+  return DLLM_OK;
 }
 
 static int block_cached_impl(const char* name, const dllm_bf16* q, const dllm_bf16* k, const dllm_bf16* v,

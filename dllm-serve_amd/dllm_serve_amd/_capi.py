@@ -39,7 +39,9 @@ SIGNATURES = {
         _I,
         [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I64, _I64, _I64, _I64, _F, _P],
     ),
+    "dllm_attn_varlen_launch_shape": (_I, [_I, _I, _I, _I, _I, _I, _P, _P, _P]),
     "dllm_attn_block_cached_workspace_size": (_SZ, [_I, _I, _I, _I, _I, _I]),
+    "dllm_attn_block_cached_launch_shape": (_I, [_I, _I, _I, _I, _I, _I, _P, _P, _P]),
     "dllm_attn_block_cached_fwd": (
         _I,
         [_P, _P, _P, _P, _P, _P, _I, _I, _I, _P, _P, _I64, _P, _P, _I, _I, _I,
@@ -183,6 +185,25 @@ def attn_block_cached_fwd_raw(q_ptr, k_ptr, v_ptr, o_ptr, cu_ptr, ids_ptr, n_seg
                                                q_st, k_st, v_st, o_st, scale, ws_ptr, ws_bytes, stream)
     if rc != DLLM_OK:
         _check(rc, "dllm_attn_block_cached_fwd")
+
+
+def varlen_launch_shape(n_seg, max_seqlen_q, max_seqlen_k, Hq, Hkv, D) -> dict:
+    """Launch shape K3a picks for these sizes (no launch): wavefronts per
+    workgroup, keys per tile, grid."""
+    vals = [ctypes.c_int(0) for _ in range(3)]
+    _check(load().dllm_attn_varlen_launch_shape(n_seg, max_seqlen_q, max_seqlen_k, Hq, Hkv, D,
+                                                *[ctypes.byref(x) for x in vals]), "dllm_attn_varlen_launch_shape")
+    return dict(wavefronts=vals[0].value, tile_keys=vals[1].value, grid=vals[2].value)
+
+
+def block_cached_launch_shape(n_seg, max_q, max_keys, Hq, Hkv, D) -> dict:
+    """Launch shape K3b picks for these sizes (no launch): row blocks per
+    workgroup, key splits, grid."""
+    vals = [ctypes.c_int(0) for _ in range(3)]
+    _check(load().dllm_attn_block_cached_launch_shape(n_seg, max_q, max_keys, Hq, Hkv, D,
+                                                      *[ctypes.byref(x) for x in vals]),
+           "dllm_attn_block_cached_launch_shape")
+    return dict(row_blocks=vals[0].value, n_split=vals[1].value, grid=vals[2].value)
 
 
 def block_cached_workspace_size(n_seg, max_q, max_keys, Hq, Hkv, D) -> int:

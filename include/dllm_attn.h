@@ -97,6 +97,16 @@ int dllm_attn_varlen_fwd(const dllm_bf16* q, const dllm_bf16* k, const dllm_bf16
                          int64_t o_stride_tok, float softmax_scale, void* stream);
 
 /*
+ * Launch shape dllm_attn_varlen_fwd picks for these sizes, without launching:
+ * wavefronts per workgroup (4, 12 or 8), keys per LDS tile and the grid (0
+ * when there is nothing to do).  No counterpart in the reference (flash-attn
+ * chooses its tiling internally); it lets tests and profiles name the kernel
+ * a given call runs.  Any output pointer may be null.
+ */
+int dllm_attn_varlen_launch_shape(int n_seg, int max_seqlen_q, int max_seqlen_k, int Hq, int Hkv, int D,
+                                  int* wavefronts, int* tile_keys, int* grid);
+
+/*
  * K3b -- attention of the current generation block against cached KV plus
  * the block itself (mode 2 / "reuse cache").  Replaces the load_kvcache +
  * torch.cat + flash_attn_varlen_func sequence of
@@ -118,6 +128,12 @@ int dllm_attn_varlen_fwd(const dllm_bf16* q, const dllm_bf16* k, const dllm_bf16
  * function returns 0).
  */
 size_t dllm_attn_block_cached_workspace_size(int n_seg, int max_q, int max_keys, int Hq, int Hkv, int D);
+/* Launch shape of dllm_attn_block_cached_fwd for these sizes, without
+ * launching: 32-row blocks per workgroup (1 or 2), key splits (> 1 adds the
+ * combine launch) and the grid.  No counterpart in the reference; for tests
+ * and profiles.  Any output pointer may be null. */
+int dllm_attn_block_cached_launch_shape(int n_seg, int max_q, int max_keys, int Hq, int Hkv, int D,
+                                        int* row_blocks, int* n_split, int* grid);
 int dllm_attn_block_cached_fwd(const dllm_bf16* q, const dllm_bf16* k, const dllm_bf16* v, dllm_bf16* o,
                                const int32_t* cu, const int32_t* seg_ids, int n_seg, int max_q, int max_keys,
                                const dllm_bf16* k_cache, const dllm_bf16* v_cache, int64_t cache_slots,

@@ -160,3 +160,22 @@ def test_sampler_refuses_cpu_tensors():
         s(torch.zeros(32, 8, dtype=torch.bfloat16), seqs, torch.zeros(2, 18, dtype=torch.int64))
     with pytest.raises(NotImplementedError):
         s(torch.zeros(32, 8, dtype=torch.bfloat16), seqs, torch.zeros(2, 18, dtype=torch.int64), remasking="topk")
+
+
+def test_launch_shape_queries():
+    """The launch shapes the benchmark workloads run (host-side planning only)."""
+    c2 = _capi.varlen_launch_shape(8, 384, 384, 32, 32, 128)
+    assert c2 == dict(wavefronts=12, tile_keys=32, grid=256)      # one workgroup per (sequence, head)
+    assert _capi.varlen_launch_shape(4, 384, 384, 32, 32, 128)["wavefronts"] == 4   # 128 pairs: < 160
+    c4 = _capi.varlen_launch_shape(4, 1280, 1280, 32, 32, 128)
+    assert c4["wavefronts"] == 4 and c4["tile_keys"] == 32 and c4["grid"] >= 4 * 32 * 10
+    assert _capi.varlen_launch_shape(2, 4096, 4096, 32, 32, 128)["wavefronts"] == 8
+    assert _capi.varlen_launch_shape(16, 1245, 1245, 28, 4, 128)["wavefronts"] == 4
+    assert _capi.varlen_launch_shape(0, 384, 384, 32, 32, 128)["grid"] == 0
+    c5 = _capi.block_cached_launch_shape(32, 32, 4128, 32, 32, 128)
+    assert c5["row_blocks"] == 1 and c5["n_split"] == 1 and c5["grid"] >= 32 * 32
+    dream = _capi.block_cached_launch_shape(16, 32, 732, 28, 4, 128)   # 7 M tiles per (segment, KV head)
+    assert dream["row_blocks"] == 2 and dream["n_split"] == 1
+    assert _capi.block_cached_launch_shape(2, 32, 4128, 32, 32, 128)["n_split"] > 1
+    with pytest.raises(RuntimeError):
+        _capi.varlen_launch_shape(1, 8, 8, 32, 32, 64)

@@ -147,6 +147,37 @@ def test_varlen_strided_views(dev):
     assert_attn_close(o, ref, "strided")
 
 
+@pytest.mark.parametrize("lens,Hq,Hkv,pad", [
+    ([150, 260, 1], 8, 2, 8),               # 4-wavefront launch
+    ([300, 384, 1, 257, 383] * 2, 16, 16, 24),  # 160 pairs of 257..384 M rows: 12-wavefront launch
+    ([2100, 40], 4, 4, 8),                  # key streams >= 2048: 8-wavefront launch
+])
+def test_varlen_token_strides_not_multiple_of_256_bytes(dev, lens, Hq, Hkv, pad):
+    """Rows padded by a multiple of 8 elements that is not a multiple of 128,
+    so a token's K row does not start on a 256-byte boundary: the K tile's
+    chunk swizzle must act on the chunk alone (an XOR over row offset + chunk
+    reads the wrong 16 bytes, or the next token's)."""
+    print(f"varlen token strides +{pad} lens={lens} Hq={Hq} Hkv={Hkv}", flush=True)
+    D = 128
+    q, k, v, cu = configs.packed_qkv(lens, Hq, Hkv, D, seed=len(lens) + pad)
+    n = q.shape[0]
+
+    def padded(t, H):
+        buf = torch.full((n, H * D + pad), float("nan"), dtype=torch.bfloat16)
+        buf[:, :H * D] = t.reshape(n, H * D)
+        return buf.to(dev)[:, :H * D].view(n, H, D)
+
+    qd, kd, vd = padded(q, Hq), padded(k, Hkv), padded(v, Hkv)
+    assert kd.stride(0) == Hkv * D + pad and (kd.stride(0) * 2) % 256 != 0
+    obuf = torch.full((n, Hq * D + pad), 7.0, dtype=torch.bfloat16, device=dev)
+    o = obuf[:, :Hq * D].view(n, Hq, D)
+    _capi.attn_varlen_fwd(qd, kd, vd, o, cu.to(dev), cu.to(dev), None, len(lens), max(lens), D ** -0.5)
+    torch.cuda.synchronize()
+    ref = oatt.varlen(to_np(q), to_np(k), to_np(v), cu.numpy(), cu.numpy(), D ** -0.5, dtype=np.float32)
+    assert_attn_close(o, ref, f"stride +{pad}")
+    assert torch.all(obuf[:, Hq * D:].float() == 7.0), "padding between output rows was written"
+
+
 def test_varlen_bad_head_dim_raises(dev):
     q = torch.zeros(8, 4, 64, dtype=torch.bfloat16, device=dev)
     cu = torch.tensor([0, 8], dtype=torch.int32, device=dev)

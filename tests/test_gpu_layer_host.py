@@ -145,11 +145,11 @@ def test_layers_of_two_head_shapes_share_one_step(dev):
                 k = torch.randn(n, Hkv, D, generator=gen).to(torch.bfloat16)
                 v = torch.randn(n, Hkv, D, generator=gen).to(torch.bfloat16)
                 ins.append((q, k, v, q.to(dev), k.to(dev), v.to(dev)))
-            plan = get_context()._dllm_plan
             ws_small = _capi.block_cached_workspace_size(2, 32, 32 + 1016, 8, 2, D)
             ws_large = _capi.block_cached_workspace_size(2, 32, 32 + 1016, 32, 8, D)
             assert 0 < ws_small < ws_large, (ws_small, ws_large)
             outs = [layers[0](*ins[0][3:]), layers[1](*ins[1][3:])]
+            plan = get_context()._dllm_plan  # built by the first layer call of the step
             sentinels = [torch.full((ws_small,), 0x5A, dtype=torch.uint8, device=dev) for _ in range(4)]
             outs.append(layers[0](*ins[0][3:]))
             torch.cuda.synchronize()

@@ -217,6 +217,29 @@ def bench_block_cached(dev, quick):
                 bytes_per_call=byts, store_us=ms_store * 1e3, store_gbs=c["store_bytes"] / (ms_store * 1e-3) / 1e9)
 
 
+def bench_mfma_probe(dev, iters=20000, reps=5):
+    """The library's register-only MFMA clock probe (one workgroup of eight
+    wavefronts per CU, four independent MFMA chains each): median TFLOP/s of
+    `reps` launches.  Its rate moves with the shader clock only, so it is
+    the same-run control for the kernel timings beside it."""
+    from dllm_serve_amd import _capi
+
+    n_cu = torch.cuda.get_device_properties(dev).multi_processor_count
+    sink = torch.empty(n_cu * 512, dtype=torch.float32, device=dev)
+    flops = _capi.mfma_probe(sink, n_cu, iters)  # untimed first launch
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(reps):
+        t = Timer()
+        t.start()
+        _capi.mfma_probe(sink, n_cu, iters)
+        times.append(t.stop_ms())
+    ms = sorted(times)[reps // 2]
+    tf = flops / (ms * 1e-3) / 1e12
+    return dict(mfma_probe_tflops=round(tf, 1), of_peak=round(tf / PEAK_BF16_TFLOPS, 4), cus=n_cu,
+                ms=round(ms, 4))
+
+
 def bench_copy(dev, nbytes=1 << 30):
     """A plain device-to-device copy of 1 GiB (torch / HIP runtime): the
     practical HBM rate the copy-like kernels (KV scatter, RoPE, block-cached
@@ -362,94 +385,104 @@ def bench_select(dev, n_layers=4):
     return out
 
 
-def bench_sparse_c4(dev, steps_block=64, quick=False, n_layers=32):
+def _block_attention_ms(dev, prompts, gen, Hq, Hkv, n_layers, cfgs, steps_block, graphed, D=128):
+    """Attention time of one block of denoising steps per layer: sequences of
+    the given prompt lengths (+ gen masked tokens), sequence i under
+    SparseConfig cfgs[i] (None: dense), n_layers Attention layers with their
+    own q/k/v and cache pages, every step through Attention.forward.
+
+    graphed: each step's tables built on the device and the step replayed
+    from a HIP graph captured once per launch shape (StepGraphs); two blocks
+    run and the second, all replays enqueued back to back, is timed with HIP
+    events around the block.  Eager: every layer call from the host, timed
+    from before each step's host plan (StepPlan) and from after it; returns
+    (ms, ms with the host plan)."""
+    from dllm_serve_amd.engine.device_step import DeviceStepState, StepGraphs
+    from dllm_serve_amd.engine.sequence import PageAllocator, Sequence, prepare_step
+    from dllm_serve_amd.layers.attention import Attention
+    from dllm_serve_amd.utils.context import get_context, reset_context
+
+    B = len(prompts)
+    attns = [Attention(Hq, D, D ** -0.5, Hkv, causal=False) for _ in range(n_layers)]
+    seqs = [Sequence([1] * P, gen, 126336, cfg, device=dev, steps=gen) for P, cfg in zip(prompts, cfgs)]
+    pages = max(1, sum(s.num_blocks for s in seqs))
+    cache = torch.zeros(2, n_layers, pages, 256, Hkv, D, dtype=torch.bfloat16, device=dev)
+    for i, a in enumerate(attns):
+        a.k_cache, a.v_cache = cache[0, i], cache[1, i]
+    alloc = PageAllocator(range(pages))
+    for s in seqs:
+        if s.sparse_state is not None:
+            alloc.allocate(s)
+    g = torch.Generator(device=dev).manual_seed(1)
+    rows_all = sum(P + gen for P in prompts)
+    full = [(torch.randn(rows_all, Hq, D, generator=g, device=dev, dtype=torch.bfloat16),
+             torch.randn(rows_all, Hkv, D, generator=g, device=dev, dtype=torch.bfloat16),
+             torch.randn(rows_all, Hkv, D, generator=g, device=dev, dtype=torch.bfloat16))
+            for _ in range(n_layers)]
+    torch.cuda.synchronize()
+    total = total_plan = 0.0
+    t_all, t = Timer(), Timer()
+    if graphed:
+        def step_fn(tables):
+            n = tables.layout.total_rows
+            for a, (q, k, v) in zip(attns, full):
+                a(q[:n], k[:n], v[:n])
+
+        tok = torch.zeros(B, max(prompts) + gen, dtype=torch.int64, device=dev)
+        sg = StepGraphs(DeviceStepState(seqs, dev, tok.stride(0)), step_fn)
+        for block in range(2):
+            if block:  # the second block's replays, enqueued back to back
+                torch.cuda.synchronize()
+                t.start()
+            for step in range(steps_block):
+                sg.run(seqs)
+                for s in seqs:
+                    s.advance()
+            if block:
+                total = t.stop_ms() / n_layers
+        del sg
+        torch.cuda.synchronize()
+        del full, cache
+        return total, None
+    for step in range(steps_block):
+        prepare_step(seqs, dev)
+        rows = sum(s.step_rows()[1] for s in seqs)
+        t_all.start()  # the GPU is idle here (the previous step ended with a synchronisation)
+        attns[0]._plan(get_context(), dev)  # per-step host plan, shared by all layers
+        t.start()
+        for a, (q, k, v) in zip(attns, full):
+            a(q[:rows], k[:rows], v[:rows])
+        total += t.stop_ms() / n_layers
+        total_plan += t_all.a.elapsed_time(t.b) / n_layers
+        reset_context()
+        for s in seqs:
+            s.advance()
+    del full, cache
+    return total, total_plan
+
+
+def bench_sparse_c4(dev, steps_block=64, n_layers=32):
     """C4 attention per 64-step block and per layer (B=4, P=1024, gen 256,
     block 64, LLaDA-8B shape): sparse = head_select retention 0.5 (1 full
     step, 1 full step + selection/store, 62 reuse steps); dense = 64 full
     recompute steps.  Each step runs the model's 32 attention layers (own
     q/k/v and cache pages each), so the per-step table work is shared as in
-    the model; the figure is the block's time divided by n_layers.
-
-    Primary figures: the steps as the device-step path runs them -- each
-    step's tables built on the device and the step replayed from a HIP graph
-    captured once per launch shape (StepGraphs).  Two blocks run; the second,
-    all replays enqueued back to back, is timed with HIP events around the
-    block.  `eager`: the
-    same block with every Attention.forward called from the host, timed from
-    before each step's host plan (StepPlan: tables built on the host and
-    copied over, shared by the step's layers) and from after it."""
-    from dllm_serve_amd.engine.device_step import DeviceStepState, StepGraphs
-    from dllm_serve_amd.engine.sequence import PageAllocator, Sequence, prepare_step
-    from dllm_serve_amd.layers.attention import Attention
+    the model; the figure is the block's time divided by n_layers.  Primary
+    figures from the device-step path (graphs), `eager` from host layer calls
+    (see _block_attention_ms)."""
     from dllm_serve_amd.sparse.state import SparseConfig
-    from dllm_serve_amd.utils.context import get_context, reset_context
 
     Hq = Hkv = 32
-    D = 128
     B, P, gen, blk = 4, 1024, 256, 64
-
-    def run(cfg, graphed):
-        attns = [Attention(Hq, D, D ** -0.5, Hkv, causal=False) for _ in range(n_layers)]
-        pages = 4 * 8
-        cache = torch.zeros(2, n_layers, pages, 256, Hkv, D, dtype=torch.bfloat16, device=dev)
-        for i, a in enumerate(attns):
-            a.k_cache, a.v_cache = cache[0, i], cache[1, i]
-        seqs = [Sequence([1] * P, gen, 126336, cfg, device=dev, steps=gen) for _ in range(B)]
-        alloc = PageAllocator(range(pages))
-        if cfg is not None:
-            for s in seqs:
-                alloc.allocate(s)
-        g = torch.Generator(device=dev).manual_seed(1)
-        full = [(torch.randn(B * (P + gen), Hq, D, generator=g, device=dev, dtype=torch.bfloat16),
-                 torch.randn(B * (P + gen), Hkv, D, generator=g, device=dev, dtype=torch.bfloat16),
-                 torch.randn(B * (P + gen), Hkv, D, generator=g, device=dev, dtype=torch.bfloat16))
-                for _ in range(n_layers)]
-        torch.cuda.synchronize()
-        total = total_plan = 0.0
-        t_all, t = Timer(), Timer()
-        if graphed:
-            def step_fn(tables):
-                n = tables.layout.total_rows
-                for a, (q, k, v) in zip(attns, full):
-                    a(q[:n], k[:n], v[:n])
-
-            tok = torch.zeros(B, P + gen, dtype=torch.int64, device=dev)
-            sg = StepGraphs(DeviceStepState(seqs, dev, tok.stride(0)), step_fn)
-            for block in range(2):
-                if block:  # the second block's replays, enqueued back to back
-                    torch.cuda.synchronize()
-                    t.start()
-                for step in range(steps_block):
-                    sg.run(seqs)
-                    for s in seqs:
-                        s.advance()
-                if block:
-                    total = t.stop_ms() / n_layers
-            del sg
-            torch.cuda.synchronize()
-            del full, cache
-            return total, None
-        for step in range(steps_block):
-            prepare_step(seqs, dev)
-            rows = sum(s.step_rows()[1] for s in seqs)
-            t_all.start()  # the GPU is idle here (the previous step ended with a synchronisation)
-            attns[0]._plan(get_context(), dev)  # per-step host plan, shared by all layers
-            t.start()
-            for a, (q, k, v) in zip(attns, full):
-                a(q[:rows], k[:rows], v[:rows])
-            total += t.stop_ms() / n_layers
-            total_plan += t_all.a.elapsed_time(t.b) / n_layers
-            reset_context()
-            for s in seqs:
-                s.advance()
-        del full, cache
-        return total, total_plan
-
     cfgs = dict(sparse=SparseConfig(enabled=True, default_block_len=blk, retention_ratio=0.5, pool_kernel=3,
                                     delay_step=1, head_select=True),
                 ret1=SparseConfig(enabled=True, default_block_len=blk, retention_ratio=1.0, pool_kernel=3,
                                   delay_step=1, head_select=True),
                 dense=None)
+
+    def run(cfg, graphed):
+        return _block_attention_ms(dev, [P] * B, gen, Hq, Hkv, n_layers, [cfg] * B, steps_block, graphed)
+
     graphed = {k: run(c, True)[0] for k, c in cfgs.items()}
     eager = {k: run(c, False) for k, c in cfgs.items()}
     out = {f"ms_per_block_{k}": v for k, v in graphed.items()}
@@ -460,6 +493,38 @@ def bench_sparse_c4(dev, steps_block=64, quick=False, n_layers=32):
               speedup_vs_ret1=eager["ret1"][0] / eager["sparse"][0],
               speedup_vs_ret1_with_host_plan=eager["ret1"][1] / eager["sparse"][1])
     out["eager"] = ea
+    return out
+
+
+def bench_sparse_dream(dev, n_layers=28):
+    """Dream-7B attention (28 layers, 28 query / 4 KV heads) per 16-step block
+    and per layer over the C3 batch: the 16 seeded prompt lengths of
+    128..1024 tokens + 256 generated tokens each, block length 16.  `mixed`
+    follows the reference's Dream test (tests/unit/test_dream_sparse.py:49):
+    sequences cycle through [dense, SparseConfig(retention 0.5, block 16),
+    dense] (token selection, the SparseConfig default); `sparse` puts every
+    sequence under that config, `ret1` under retention 1.0, `dense` under
+    none.  A 16-step block of a sparse sequence is one full step, one full
+    step with selection and store, and 14 reuse steps.  Device-step path
+    (graphs), as in bench_sparse_c4."""
+    from oracle.configs import c3_lens
+    from dllm_serve_amd.sparse.state import SparseConfig
+
+    gen, blk = 256, 16
+    prompts = [n - gen for n in c3_lens()]
+    sp = SparseConfig(enabled=True, retention_ratio=0.5, default_block_len=blk)
+    r1 = SparseConfig(enabled=True, retention_ratio=1.0, default_block_len=blk)
+    B = len(prompts)
+    cfgs = dict(mixed=[sp if i % 3 == 1 else None for i in range(B)], sparse=[sp] * B, ret1=[r1] * B,
+                dense=[None] * B)
+    ms = {k: _block_attention_ms(dev, prompts, gen, 28, 4, n_layers, c, blk, True)[0] for k, c in cfgs.items()}
+    out = {f"ms_per_block_{k}": v for k, v in ms.items()}
+    # tokens a block of the batch generates: gen / (gen / blk) = blk per sequence
+    out.update(speedup_sparse_vs_dense=ms["dense"] / ms["sparse"], speedup_sparse_vs_ret1=ms["ret1"] / ms["sparse"],
+               speedup_mixed_vs_dense=ms["dense"] / ms["mixed"],
+               attention_tokens_per_s_mixed=B * blk / (ms["mixed"] * n_layers * 1e-3),
+               attention_tokens_per_s_dense=B * blk / (ms["dense"] * n_layers * 1e-3),
+               n_sparse_in_mixed=sum(c is not None for c in cfgs["mixed"]), block_len=blk, layers=n_layers)
     return out
 
 
@@ -1097,6 +1162,8 @@ def main() -> None:
         return
     log("headline: C2 dense step attention, 32 layers x 8 x 384 tokens")
     r = bench_dense(lens, Hq, Hkv, D, n_layers, args.steps, args.warmup, dev)
+    log("clock control: register-only MFMA probe")
+    clock = bench_mfma_probe(dev)
     extra = {}
     if not args.quick:
         log("C3: Dream-7B GQA 28/4 varlen")
@@ -1123,6 +1190,9 @@ def main() -> None:
                                for k, v in bench_sampler(dev).items()}
         log("C4: sparse vs dense attention per 64-step block")
         r4s = bench_sparse_c4(dev)
+        log("C3 Dream: mixed / sparse / dense attention per 16-step block")
+        extra["c3_dream_sparse_per_block"] = {k: round(v, 3) if isinstance(v, float) else v
+                                              for k, v in bench_sparse_dream(dev).items()}
         extra["c4_head_sparse_per_block"] = {k: (round(v, 3) if not isinstance(v, dict) else
                                                  {kk: round(vv, 3) for kk, vv in v.items()}) for k, v in r4s.items()}
         log("K3b at the denoise-loop reuse shapes (8 layers' caches rotated)")
@@ -1177,6 +1247,7 @@ def main() -> None:
                          algorithmic_bytes_per_launch=r["bytes_per_call"],
                          arithmetic_intensity=round(intensity, 1), machine_balance=round(balance, 1),
                          kernel_tflops=round(r["tflops_kernel"], 2), mfma_frac=round(mfma_frac, 4)),
+        "clock_control": clock,
         "cpu_baseline": cpu,
         "gpu_settle_s": SETTLE_S,
     }

@@ -66,6 +66,8 @@ SIGNATURES = {
     "dllm_lowconf_unmask": (_I, [_P, _I64, _P, _I, _I, _P, _P, _I64, _I64, _P, _P]),
     "dllm_step_build": (_I, [_P, _P, _P, _P, _I, _I64, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _P, _P, _I, _P, _P]),
     "dllm_step_advance": (_I, [_P, _I, _P]),
+    "dllm_mfma_probe_flops": (_I64, [_I, _I]),
+    "dllm_mfma_probe": (_I, [_P, _I, _I, _P]),
 }
 
 _lib = None
@@ -351,3 +353,12 @@ def step_advance(state, n_seq):
     _require_gpu(state)
     rc = load().dllm_step_advance(state.data_ptr(), n_seq, _stream(state.device))
     _check(rc, "dllm_step_advance")
+
+
+def mfma_probe(sink, n_cu: int, iters: int) -> int:
+    """Launch the register-only MFMA clock probe on the current stream;
+    returns its FLOPs (sink: float32 [n_cu * 512] on the device)."""
+    _require_gpu(sink)
+    lib = load()
+    _check(lib.dllm_mfma_probe(sink.data_ptr(), n_cu, iters, _stream(sink.device)), "dllm_mfma_probe")
+    return int(lib.dllm_mfma_probe_flops(n_cu, iters))

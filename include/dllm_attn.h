@@ -349,6 +349,17 @@ int dllm_step_build(const int32_t* seq_state, const double* ratio, const int32_t
  */
 int dllm_step_advance(int32_t* seq_state, int n_seq, void* stream);
 
+/*
+ * Same-run clock control for benchmarks.  No counterpart in the reference:
+ * a register-only MFMA loop (n_cu workgroups of 8 wavefronts, one per CU,
+ * each wavefront 4 independent v_mfma_f32_32x32x16_bf16 chains of `iters`
+ * steps) whose throughput depends only on the matrix pipe and the shader
+ * clock; a benchmark reports its TFLOP/s beside the kernels it times.
+ * sink: n_cu * 512 floats.  dllm_mfma_probe_flops gives the FLOPs of one call.
+ */
+int64_t dllm_mfma_probe_flops(int n_cu, int iters);
+int dllm_mfma_probe(float* sink, int n_cu, int iters, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -86,3 +86,56 @@ def test_three_steps_mixed_batch(dev, Hq, Hkv):
         reset_context()
         for s in seqs:
             s.advance()
+
+
+def test_dream_reference_batch_three_steps(dev):
+    """The batch of the reference's Dream sparse test
+    (tests/unit/test_dream_sparse.py:49): [dense, SparseConfig(enabled=True,
+    retention_ratio=0.5, default_block_len=16), dense] -- token selection
+    (head_select False, the SparseConfig default), pool 3, delay 1 -- at
+    Dream-7B's 28 query / 4 KV heads, gen 64.  Step 0 all full attention,
+    step 1 the middle sequence selects and stores (cache state 1), step 2 it
+    attends from its 16-token block to the cache (state 2).  Outputs within
+    the bf16 tolerance of the fp32 oracle, the cache bit-exact."""
+    Hq, Hkv, D = 28, 4, 128
+    print("layer: Dream reference batch [None, SparseConfig(0.5, block 16), None], three steps", flush=True)
+    scale = D ** -0.5
+    attn = Attention(Hq, D, scale, Hkv, causal=False)
+    n_pages = 4
+    cache = torch.zeros(2, n_pages, 256, Hkv, D, dtype=torch.bfloat16, device=dev)
+    attn.k_cache, attn.v_cache = cache[0], cache[1]
+    ref_cache = np.zeros((2, n_pages * 256, Hkv * D), dtype=np.float32)
+    cfg = SparseConfig(enabled=True, retention_ratio=0.5, default_block_len=16)
+    assert cfg.head_select is False and cfg.pool_kernel == 3 and cfg.delay_step == 1
+    P = [57, 130, 96]
+    seqs = [Sequence([5] * P[0], 64, MASK, None, device=dev), Sequence([6] * P[1], 64, MASK, cfg, device=dev),
+            Sequence([7] * P[2], 64, MASK, None, device=dev)]
+    PageAllocator([3, 1, 0, 2]).allocate(seqs[1])
+    N = [p + 64 for p in P]
+    n_keep = int((N[1] - 16) * 0.5)   # candidates: every row but the 16-token block
+    slots = list(range(3 * 256, 3 * 256 + 89))
+    rows = {0: N, 1: N, 2: [N[0], 16, N[2]]}
+    g = torch.Generator().manual_seed(49)
+    for step in range(3):
+        prepare_step(seqs, dev)
+        if step > 0:  # slot lists exist in cache states 1 and 2 (the reference raises otherwise)
+            assert n_keep == 89 and slot_mapping_for(seqs[1]) == slots
+        n = sum(rows[step])
+        q = torch.randn(n, Hq, D, generator=g).to(torch.bfloat16)
+        k = torch.randn(n, Hkv, D, generator=g).to(torch.bfloat16)
+        v = torch.randn(n, Hkv, D, generator=g).to(torch.bfloat16)
+        out = attn(q.to(dev), k.to(dev), v.to(dev))
+        torch.cuda.synchronize()
+        mid = (dict(mode=0, rows=N[1]) if step == 0 else
+               dict(mode=1, rows=N[1], blk_start=P[1], blk_len=16, n_keep=n_keep, head_select=False, pool_k=3)
+               if step == 1 else dict(mode=2, rows=16))
+        desc = [dict(mode=0, rows=N[0]), mid, dict(mode=0, rows=N[2])]
+        ref, _ = oatt.mixed_step(to_np(q), to_np(k), to_np(v), desc,
+                                 ref_cache[0].reshape(-1, Hkv, D), ref_cache[1].reshape(-1, Hkv, D),
+                                 [[], slots, []], scale, dtype=np.float32)
+        assert_attn_close(out.view(n, Hq, D), ref, f"Dream reference batch, step {step}")
+        assert np.array_equal(bits(cache[0]).reshape(-1, Hkv * D), f32_to_bf16_bits(ref_cache[0]))
+        assert np.array_equal(bits(cache[1]).reshape(-1, Hkv * D), f32_to_bf16_bits(ref_cache[1]))
+        reset_context()
+        for s in seqs:
+            s.advance()

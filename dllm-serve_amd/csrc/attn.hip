@@ -47,6 +47,7 @@ struct AttnArgs {
   const int32_t* slots;
   const int32_t* slot_off;
   float* ws;          // split partials (K3b, n_split > 1)
+  int max_pages;      // K3b paged form: row stride of the page table (its rows come in `slots`)
   int64_t q_stride, k_stride, v_stride, o_stride;
   int64_t cache_slots;
   int n_seg, Hkv, g, mtiles, n_split, keys_per_split;
@@ -721,7 +722,15 @@ __device__ __forceinline__ void cached_tile(const uint8_t* Ks, const uint8_t* Vs
 // Two wavefronts per SIMD as the register budget: the whole state then stays
 // in VGPRs (with a budget of 512 the compiler moves the O^T accumulators
 // between AGPRs and VGPRs around every softmax rescale).
-template <int RB>
+// PAGED: the cached rows of segment s are given by a page table instead of a
+// slot list -- `slot_off` holds cached_len (int32 per segment) and `slots`
+// the page table ([n_seg][max_pages] int32 page ids, 256-row pages): cached
+// row r sits in cache row page_table[s][r / 256] * 256 + r % 256.  A 128-key
+// tile starts at a multiple of 128, so its cached rows lie in one page.  Each
+// wavefront DMAs its own copy of the page ids of its key range (up to 64) at
+// the start, next to Q -- no wavefront waits for another -- so its first K/V
+// tiles wait on one load instead of two (slot offsets, then the slot list).
+template <int RB, bool PAGED>
 // The launch geometry and the tables the first, dependent loads read come as
 // leading scalar arguments (14 dwords): the library is built with kernel
 // argument preloading, so they are in SGPRs when a wave starts instead of one
@@ -747,8 +756,8 @@ __global__ __launch_bounds__(256 * RB) __attribute__((amdgpu_waves_per_eu(2, 2))
   // known, so that those two dependent loads overlap.
   // (The scalar loads of the segment's offsets all come first: a load after
   // the first DMA into LDS could no longer be a scalar one.)
-  const int slot_base = slot_off[s];
-  const int n_c = slot_off[s + 1] - slot_base;
+  const int slot_base = PAGED ? 0 : slot_off[s];
+  const int n_c = PAGED ? max(slot_off[s], 0) : slot_off[s + 1] - slot_base;
   const int kbeg0 = split * keys_per_split;  // this split's first key (past Lk: no tiles)
   const int sid = seg_ids ? seg_ids[s] : s;
   const int qrow0 = cu_q[sid];
@@ -773,8 +782,11 @@ __global__ __launch_bounds__(256 * RB) __attribute__((amdgpu_waves_per_eu(2, 2))
   const int64_t row_elems = (int64_t)Hkv * HD;
   // without a cache (cache_slots = 0, slots may be null) every cached row is
   // outside it: the fetches then read slot_off[0], a valid dummy
-  const bool have_slots = n_c > 0 && slots != nullptr && a.cache_slots > 0;
-  const int32_t* sp = have_slots ? slots + slot_base : slot_off;
+  const bool have_slots = n_c > 0 && slots != nullptr && a.cache_slots > 0 && (!PAGED || a.max_pages > 0);
+  const int32_t* sp = have_slots ? slots + (PAGED ? (int64_t)s * a.max_pages : (int64_t)slot_base) : slot_off;
+  // paged: page ids [pg0, pg0 + 256 RB) of the segment's row, one per lane of
+  // every wavefront, in the ring (ids past the row read a valid dummy)
+  const int pg0 = kbeg0 >> 8;
   // Per-wave pipeline: the slots of tile t+2 are fetched before tile t+1's
   // DMA is issued, so that after computing tile t the wave can issue tile
   // t+2 into the stage it just freed while tile t+1 is still in flight --
@@ -792,11 +804,41 @@ __global__ __launch_bounds__(256 * RB) __attribute__((amdgpu_waves_per_eu(2, 2))
     __builtin_amdgcn_global_load_lds(
         src, (__attribute__((address_space(3))) void*)(slot_ring + ((t & 3) * 4 * RB + wave_id) * 64), 4, 0, 0);
   };
+  // Each wavefront's page ids sit in the upper half of the ring: the merge at
+  // the end parks every row block's m / l in its first 256 RB words while
+  // other wavefronts may still read page ids for their last tiles.
+  uint32_t* const page_ring = slot_ring + 512 * RB + wave_id * 64;
+  auto fetch_pages = [&]() {
+    const int idx = pg0 + lane;
+    const int32_t* src = have_slots && idx < a.max_pages ? sp + idx : (have_slots ? sp : slot_off);
+    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)page_ring, 4, 0, 0);
+  };
+  // After the prologue's wait lane l holds page id pg0 + l in a register, and
+  // the page of a tile (the same for the whole wavefront) is one lane read.
+  int page_reg = 0;
+  const uint32_t n_pages = (uint32_t)min(a.cache_slots >> 8, (int64_t)1 << 23);
+  // the first cache row of tile t's page, or -1 past the page table or for a
+  // page id outside the cache (whose rows are then masked)
+  auto page_of = [&](int t) -> int {
+    const int pg = (kbeg0 + t * CK_TILE) >> 8;
+    const int pid = __builtin_amdgcn_readlane(page_reg, (pg - pg0) & 63);
+    return have_slots && pg < a.max_pages && (uint32_t)pid < n_pages ? pid * 256 : -1;
+  };
   // this lane's slots of tile t (rows 4 (jb + j) + rl of the wave's 32); call after the wait
   auto read_slots = [&](int t, int (&dst)[NJ]) {
-    const uint32_t* e = slot_ring + ((t & 3) * 4 * RB + wave_id) * 64;
+    if constexpr (PAGED) {
+      const int row0 = page_of(t);
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) dst[j] = (int)e[4 * (jb + j) + rl];
+      for (int j = 0; j < NJ; ++j) {
+        const int kidx = kbeg0 + t * CK_TILE + 32 * wave + 4 * (jb + j) + rl;
+        // a page outside the cache leaves the slot outside too (masked below)
+        dst[j] = row0 >= 0 ? row0 + (kidx & 255) : -1;
+      }
+    } else {
+      const uint32_t* e = slot_ring + ((t & 3) * 4 * RB + wave_id) * 64;
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) dst[j] = (int)e[4 * (jb + j) + rl];
+    }
   };
   // ---- prologue: the slots of the first three tiles, then the Q^T
   // fragments (their address needs the segment's rows); D(0) and D(1) are
@@ -804,10 +846,14 @@ __global__ __launch_bounds__(256 * RB) __attribute__((amdgpu_waves_per_eu(2, 2))
   // wait that retires q follows them (so the compiler's own wait tracking
   // has no q load left to wait for inside the tile loop).  Slot fetches
   // past the key range read a clamped, valid index and go unused.
-  fetch_slots(0);
-  fetch_slots(1);
-  fetch_slots(2);
-  asm volatile("" ::: "memory");  // the slot fetches stay the oldest operations
+  if constexpr (PAGED) {
+    fetch_pages();
+  } else {
+    fetch_slots(0);
+    fetch_slots(1);
+    fetch_slots(2);
+  }
+  asm volatile("" ::: "memory");  // the slot / page fetches stay the oldest operations
   const int g = a.g;
   const int M = Lq * g;
   if (mb * RB * 32 >= M) {  // the whole workgroup: no live row block
@@ -852,7 +898,12 @@ __global__ __launch_bounds__(256 * RB) __attribute__((amdgpu_waves_per_eu(2, 2))
   // mask (bit = key within the block), from the slot ring after the wait
   auto invalid_keys = [&](int t) -> uint32_t {
     const int kidx = kbeg + t * CK_TILE + 32 * wave + lrow;
-    const uint32_t sl = slot_ring[((t & 3) * 4 * RB + wave_id) * 64 + lrow];
+    uint32_t sl;
+    if constexpr (PAGED) {
+      sl = (uint32_t)page_of(t);
+    } else {
+      sl = slot_ring[((t & 3) * 4 * RB + wave_id) * 64 + lrow];
+    }
     const bool bad = kidx < n_c && kidx < kend && sl >= n_slots;
     return (uint32_t)__builtin_amdgcn_ballot_w64(bad);
   };
@@ -872,7 +923,9 @@ __global__ __launch_bounds__(256 * RB) __attribute__((amdgpu_waves_per_eu(2, 2))
   }
   const int ntiles = (kend - kbeg + CK_TILE - 1) / CK_TILE;
   uint32_t bad_t0 = 0, bad_t1 = 0;  // invalid-key masks of tiles t and t+1
-  vm_wait<8>();  // S(0..2); the eight q loads may be outstanding
+  vm_wait<8>();  // S(0..2) or the page ids; the eight q loads may be outstanding
+  if constexpr (PAGED) page_reg = (int)page_ring[lane];
+
   int s0[NJ], s1[NJ];
   read_slots(0, s0);
   read_slots(1, s1);
@@ -904,7 +957,7 @@ __global__ __launch_bounds__(256 * RB) __attribute__((amdgpu_waves_per_eu(2, 2))
     // follows D(0) (the prologue retired S(2) before issuing both).
     if (t + 1 >= ntiles)
       vm_wait<0>();
-    else if (t == 0 || t + 2 >= ntiles)
+    else if (PAGED || t == 0 || t + 2 >= ntiles)
       vm_wait<2 * NJ>();
     else
       vm_wait<2 * NJ + 1>();
@@ -919,11 +972,11 @@ __global__ __launch_bounds__(256 * RB) __attribute__((amdgpu_waves_per_eu(2, 2))
       // stage t&1 is free again (with RB > 1 once both row blocks are done
       // with it): issue D(t+2) there, after S(t+3) (S(t+2) landed behind D(t+1))
       if constexpr (RB > 1) lds_barrier();
-      vm_wait<2 * NJ>();  // S(t+2); D(t+1) may stay in flight
+      if constexpr (!PAGED) vm_wait<2 * NJ>();  // S(t+2); D(t+1) may stay in flight
       int cur_slots[NJ];
       read_slots(t + 2, cur_slots);
       bad_t2 = invalid_keys(t + 2);
-      if (t + 3 < ntiles) fetch_slots(t + 3);
+      if (!PAGED && t + 3 < ntiles) fetch_slots(t + 3);
       issue(lds + (t & 1) * CK_STAGE, k0 + 2 * CK_TILE, cur_slots);
     }
     bad_t0 = bad_t1;
@@ -1154,6 +1207,10 @@ static int block_cached_plan(int n_seg, int max_q, int max_keys, int Hq, int Hkv
   const int tiles_per_split = (tiles + n_split - 1) / n_split;
   keys_per_split = tiles_per_split * CK_TILE;
   if (keys_per_split <= 0) keys_per_split = CK_TILE;
+  // a split's keys span at most 64 pages of 256 rows: the page-table form
+  // keeps that many page ids per wavefront in LDS (both forms plan alike, so
+  // one workspace size serves both)
+  if (keys_per_split > 64 * 256 - 256) keys_per_split = 64 * 256 - 256;
   n_split = max_keys > 0 ? (max_keys + keys_per_split - 1) / keys_per_split : 1;
   return 0;
 }
@@ -1184,12 +1241,16 @@ extern "C" int dllm_attn_block_cached_launch_shape(int n_seg, int max_q, int max
   return DLLM_OK;
 }
 
+// Slot-list form (paged = false): slots / slot_off as documented for
+// dllm_attn_block_cached_fwd.  Page-table form (paged = true): `slots` is the
+// [n_seg][max_pages] page table, `slot_off` the per-segment cached lengths.
 static int block_cached_impl(const char* name, const dllm_bf16* q, const dllm_bf16* k, const dllm_bf16* v,
                              dllm_bf16* o, const int32_t* cu, const int32_t* seg_ids, int n_seg, int max_q,
                              int max_keys, const dllm_bf16* k_cache, const dllm_bf16* v_cache, int64_t cache_slots,
                              const int32_t* slots, const int32_t* slot_off, int Hq, int Hkv, int D,
                              int64_t q_stride_tok, int64_t k_stride_tok, int64_t v_stride_tok, int64_t o_stride_tok,
-                             float softmax_scale, void* workspace, size_t workspace_bytes, void* stream) {
+                             float softmax_scale, void* workspace, size_t workspace_bytes, void* stream,
+                             bool paged = false, int max_pages = 0) {
   int rc = common_checks(name, q, k, v, o, Hq, Hkv, D, q_stride_tok, k_stride_tok, v_stride_tok, o_stride_tok);
   if (rc) return rc;
   if (n_seg < 0 || max_q < 0 || max_keys < 0) return fail(DLLM_ERR_INVALID_ARG, "%s: negative size", name);
@@ -1200,7 +1261,12 @@ static int block_cached_impl(const char* name, const dllm_bf16* q, const dllm_bf
   if (k_stride_tok * 2 >= ((int64_t)1 << 32) || v_stride_tok * 2 >= ((int64_t)1 << 32))
     return fail(DLLM_ERR_UNSUPPORTED, "%s: k / v token strides must be below 4 GiB", name);
   if (cache_slots > 0 && (!k_cache || !v_cache || !slots))
-    return fail(DLLM_ERR_INVALID_ARG, "%s: null cache / slots", name);
+    return fail(DLLM_ERR_INVALID_ARG, "%s: null cache / %s", name, paged ? "page table" : "slots");
+  if (paged && (max_pages < 0 || (cache_slots > 0 && max_pages == 0) || cache_slots % 256))
+    return fail(DLLM_ERR_INVALID_ARG, "%s: max_pages %d, cache rows %lld: the cache must be whole 256-row pages",
+                name, max_pages, (long long)cache_slots);
+  if (paged && (int64_t)n_seg * max_pages >= ((int64_t)1 << 31))
+    return fail(DLLM_ERR_INVALID_ARG, "%s: page table too large", name);
   if (cache_slots > 0 && (!aligned16(k_cache) || !aligned16(v_cache)))
     return fail(DLLM_ERR_INVALID_ARG, "%s: caches must be 16-byte aligned", name);
   AttnArgs a = {};
@@ -1209,6 +1275,7 @@ static int block_cached_impl(const char* name, const dllm_bf16* q, const dllm_bf
   a.cu_q = cu; a.cu_k = cu; a.seg_ids = seg_ids; a.slots = slots; a.slot_off = slot_off;
   a.q_stride = q_stride_tok; a.k_stride = k_stride_tok; a.v_stride = v_stride_tok; a.o_stride = o_stride_tok;
   a.n_seg = n_seg; a.Hkv = Hkv; a.g = Hq / Hkv;
+  a.max_pages = paged ? max_pages : 0;
   int mtiles, rb, n_split, kps;
   block_cached_plan(n_seg, max_q, max_keys, Hq, Hkv, mtiles, rb, n_split, kps);
   a.mtiles = mtiles; a.n_split = n_split; a.keys_per_split = kps;
@@ -1232,19 +1299,20 @@ static int block_cached_impl(const char* name, const dllm_bf16* q, const dllm_bf
   a.xcd_chunk = (int)(per_pair < 16 ? per_pair : 16);
   const int64_t grain = 8 * (int64_t)a.xcd_chunk;
   const int nb = (int)((logical + grain - 1) / grain * grain);
-  if (rb == 2) {
-    constexpr int lds_bytes = ck_lds_bytes(2);
-    if ((rc = set_lds(attn_cached_kernel<2>, lds_bytes, name))) return rc;
-    attn_cached_kernel<2><<<dim3(nb), dim3(512), lds_bytes, st>>>(a.slot_off, a.seg_ids, a.cu_q, a.slots, a.xcd_chunk,
-                                                                  a.logical_blocks, a.mtiles, a.n_split, a.Hkv,
-                                                                  a.keys_per_split, a);
-  } else {
-    constexpr int lds_bytes = ck_lds_bytes(1);
-    if ((rc = set_lds(attn_cached_kernel<1>, lds_bytes, name))) return rc;
-    attn_cached_kernel<1><<<dim3(nb), dim3(256), lds_bytes, st>>>(a.slot_off, a.seg_ids, a.cu_q, a.slots, a.xcd_chunk,
-                                                                  a.logical_blocks, a.mtiles, a.n_split, a.Hkv,
-                                                                  a.keys_per_split, a);
-  }
+  auto launch = [&](auto kern, int threads, int lds_bytes) -> int {
+    int r = set_lds(kern, lds_bytes, name);
+    if (r) return r;
+    kern<<<dim3(nb), dim3(threads), lds_bytes, st>>>(a.slot_off, a.seg_ids, a.cu_q, a.slots, a.xcd_chunk,
+                                                      a.logical_blocks, a.mtiles, a.n_split, a.Hkv, a.keys_per_split, a);
+    return DLLM_OK;
+  };
+  if (rb == 2)
+    rc = paged ? launch(attn_cached_kernel<2, true>, 512, ck_lds_bytes(2))
+               : launch(attn_cached_kernel<2, false>, 512, ck_lds_bytes(2));
+  else
+    rc = paged ? launch(attn_cached_kernel<1, true>, 256, ck_lds_bytes(1))
+               : launch(attn_cached_kernel<1, false>, 256, ck_lds_bytes(1));
+  if (rc) return rc;
   if ((rc = check_launch(name))) return rc;
   if (n_split > 1) {
     const int64_t rows = (int64_t)n_seg * Hkv * a.mtiles * 32;
@@ -1264,6 +1332,23 @@ extern "C" int dllm_attn_block_cached_fwd(const dllm_bf16* q, const dllm_bf16* k
   return block_cached_impl("dllm_attn_block_cached_fwd", q, k, v, o, cu, seg_ids, n_seg, max_q, max_keys, k_cache,
                            v_cache, cache_slots, slots, slot_off, Hq, Hkv, D, q_stride_tok, k_stride_tok,
                            v_stride_tok, o_stride_tok, softmax_scale, workspace, workspace_bytes, stream);
+}
+
+extern "C" int dllm_attn_block_cached_paged_fwd(const dllm_bf16* q, const dllm_bf16* k, const dllm_bf16* v,
+                                                dllm_bf16* o, const int32_t* cu, const int32_t* seg_ids, int n_seg,
+                                                int max_q, int max_keys, const dllm_bf16* k_cache,
+                                                const dllm_bf16* v_cache, int num_pages, const int32_t* page_table,
+                                                int max_pages, const int32_t* cached_len, int Hq, int Hkv, int D,
+                                                int64_t q_stride_tok, int64_t k_stride_tok, int64_t v_stride_tok,
+                                                int64_t o_stride_tok, float softmax_scale, void* workspace,
+                                                size_t workspace_bytes, void* stream) {
+  const char* name = "dllm_attn_block_cached_paged_fwd";
+  if (num_pages < 0) return fail(DLLM_ERR_INVALID_ARG, "%s: negative num_pages", name);
+  if (!cached_len && n_seg > 0) return fail(DLLM_ERR_INVALID_ARG, "%s: null cached_len", name);
+  return block_cached_impl(name, q, k, v, o, cu, seg_ids, n_seg, max_q, max_keys, k_cache, v_cache,
+                           (int64_t)num_pages * 256, page_table, cached_len, Hq, Hkv, D, q_stride_tok, k_stride_tok,
+                           v_stride_tok, o_stride_tok, softmax_scale, workspace, workspace_bytes, stream, true,
+                           max_pages);
 }
 
 // ---------------------------------------------------------------------------

@@ -47,6 +47,11 @@ SIGNATURES = {
         [_P, _P, _P, _P, _P, _P, _I, _I, _I, _P, _P, _I64, _P, _P, _I, _I, _I,
          _I64, _I64, _I64, _I64, _F, _P, _SZ, _P],
     ),
+    "dllm_attn_block_cached_paged_fwd": (
+        _I,
+        [_P, _P, _P, _P, _P, _P, _I, _I, _I, _P, _P, _I, _P, _I, _P, _I, _I, _I,
+         _I64, _I64, _I64, _I64, _F, _P, _SZ, _P],
+    ),
     "dllm_attn_block_cached_noalloc_max_workspace": (_SZ, []),
     "dllm_attn_block_cached_fwd_noalloc": (
         _I,
@@ -230,6 +235,39 @@ def attn_block_cached_fwd(q, k, v, o, cu, seg_ids, n_seg, max_q, max_keys,
         q.stride(0), k.stride(0), v.stride(0), o.stride(0), float(scale),
         _ptr(workspace), ws_bytes, _stream(q.device))
     _check(rc, "dllm_attn_block_cached_fwd")
+
+
+def attn_block_cached_paged_fwd_raw(q_ptr, k_ptr, v_ptr, o_ptr, cu_ptr, ids_ptr, n_seg, max_q, max_keys, kc_ptr,
+                                    vc_ptr, num_pages, pt_ptr, max_pages, len_ptr, Hq, Hkv, D, q_st, k_st, v_st, o_st,
+                                    scale, ws_ptr, ws_bytes, stream) -> None:
+    """attn_block_cached_paged_fwd over device addresses (see attn_varlen_fwd_raw)."""
+    rc = _lib_now().dllm_attn_block_cached_paged_fwd(q_ptr, k_ptr, v_ptr, o_ptr, cu_ptr, ids_ptr, n_seg, max_q,
+                                                     max_keys, kc_ptr, vc_ptr, num_pages, pt_ptr, max_pages, len_ptr,
+                                                     Hq, Hkv, D, q_st, k_st, v_st, o_st, scale, ws_ptr, ws_bytes,
+                                                     stream)
+    if rc != DLLM_OK:
+        _check(rc, "dllm_attn_block_cached_paged_fwd")
+
+
+def attn_block_cached_paged_fwd(q, k, v, o, cu, seg_ids, n_seg, max_q, max_keys, k_cache, v_cache, page_table,
+                                cached_len, scale, workspace):
+    """K3b, page-table form: segment s's cached rows are rows r < cached_len[s]
+    of its pages page_table[s, r // 256] (256-row pages of the cache, given
+    as [num_pages, 256, Hkv, D] or flat rows)."""
+    _require_gpu(q, k, v, o, cu, page_table, cached_len)
+    lib = load()
+    Hkv, D = k.shape[1], k.shape[2]
+    rows = (min(k_cache.numel(), v_cache.numel()) // (Hkv * D)
+            if k_cache is not None and v_cache is not None and k_cache.numel() else 0)
+    num_pages = rows // 256
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    rc = lib.dllm_attn_block_cached_paged_fwd(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), cu.data_ptr(), _ptr(seg_ids), n_seg, max_q,
+        max_keys, _ptr(k_cache) if num_pages else None, _ptr(v_cache) if num_pages else None, num_pages,
+        page_table.data_ptr(), page_table.shape[1] if page_table.dim() == 2 else page_table.numel() // max(n_seg, 1),
+        cached_len.data_ptr(), q.shape[1], Hkv, D, q.stride(0), k.stride(0), v.stride(0), o.stride(0), float(scale),
+        _ptr(workspace), ws_bytes, _stream(q.device))
+    _check(rc, "dllm_attn_block_cached_paged_fwd")
 
 
 def block_cached_noalloc_max_workspace() -> int:

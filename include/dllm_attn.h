@@ -144,6 +144,35 @@ int dllm_attn_block_cached_fwd(const dllm_bf16* q, const dllm_bf16* k, const dll
                                void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * K3b, page-table form: the cached rows of each segment are given the way
+ * the runner holds them, as a page table and a length, instead of a slot
+ * list.  The signature the boundary of the hot path names for this kernel
+ * (page_table, max_pages, cached_len); the rows are those the reference's
+ * state-2 slot list addresses (dllmserve/engine/model_runner.py:257-273:
+ * concatenation over pages j of page_j * 256 + 0..255, the last page
+ * partly), read by load_kvcache and concatenated with the block
+ * (dllmserve/layers/attention.py:235-265).
+ *
+ * Segment s (the s-th of the launch, as for slot_off) has cached_len[s]
+ * cached rows; cached row r is cache row page_table[s * max_pages + r / 256]
+ * * 256 + r % 256, in a cache of num_pages pages of 256 rows ([num_pages *
+ * 256, Hkv, D], the reference's [num_blocks, 256, Hkv, D]).  A row whose page
+ * id is outside [0, num_pages), or whose page index is >= max_pages, is left
+ * out of the softmax.  Same workspace (dllm_attn_block_cached_workspace_size)
+ * and results as dllm_attn_block_cached_fwd over the equivalent slot lists;
+ * the kernel needs one dependent load (the page ids) before its first K/V
+ * tile instead of two (slot offsets, then the slot list).
+ */
+int dllm_attn_block_cached_paged_fwd(const dllm_bf16* q, const dllm_bf16* k, const dllm_bf16* v, dllm_bf16* o,
+                                     const int32_t* cu, const int32_t* seg_ids, int n_seg, int max_q, int max_keys,
+                                     const dllm_bf16* k_cache, const dllm_bf16* v_cache, int num_pages,
+                                     const int32_t* page_table, int max_pages, const int32_t* cached_len,
+                                     int Hq, int Hkv, int D,
+                                     int64_t q_stride_tok, int64_t k_stride_tok, int64_t v_stride_tok,
+                                     int64_t o_stride_tok, float softmax_scale,
+                                     void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * K3b without a caller workspace.  No counterpart in the reference: this is
  * for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops, harnesses that forbid allocation).  Same

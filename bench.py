@@ -1108,21 +1108,44 @@ def profile_denoise_run(dev):
 
 
 TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "attn_dense_kernel_llada_c2_8x384_counters.md")
+KERNEL_SOURCE = os.path.join(ROOT, "dllm-serve_amd", "csrc", "attn.hip")
+
+
+def kernel_source_sha256() -> str:
+    """First 16 hex digits of the SHA-256 of the attention kernels' source file."""
+    import hashlib
+    with open(KERNEL_SOURCE, "rb") as f:
+        return hashlib.sha256(f.read()).hexdigest()[:16]
 
 
 def measured_traffic(kernel: str):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE /
-    WRITE_SIZE summary (counters scaled by a plain 256 MiB copy), or None."""
+    WRITE_SIZE summary (counters scaled by a plain 256 MiB copy), and where that
+    figure was recorded: the summary's `recorded_on:` line names the commit and
+    the SHA-256 of `attn.hip` of the build the counters ran on, which is compared
+    with the source this run loads.  Returns (bytes or None, provenance dict)."""
+    prov = {"summary": os.path.relpath(TRAFFIC_SUMMARY, ROOT), "commit": None,
+            "kernel_source_sha256": None, "current_kernel_source_sha256": kernel_source_sha256()}
     try:
         text = open(TRAFFIC_SUMMARY).read()
     except OSError:
-        return None
-    if kernel not in text.splitlines()[0]:
-        return None
-    for line in text.splitlines():
+        return None, prov
+    lines = text.splitlines()
+    if kernel not in lines[0]:
+        return None, prov
+    traffic = None
+    for line in lines:
         if line.startswith("traffic_bytes_per_launch:"):
-            return int(line.split(":")[1].strip())
-    return None
+            traffic = int(line.split(":")[1].strip())
+        elif line.startswith("recorded_on:"):
+            for part in line.split(":", 1)[1].split(";"):
+                key, _, val = part.strip().partition(" ")
+                if key == "commit":
+                    prov["commit"] = val.strip()
+                elif key == "attn.hip_sha256":
+                    prov["kernel_source_sha256"] = val.strip()
+    prov["source_matches"] = prov["kernel_source_sha256"] == prov["current_kernel_source_sha256"]
+    return traffic, prov
 
 
 def main() -> None:
@@ -1226,6 +1249,7 @@ def main() -> None:
     else:
         roof = {"bound": "mfma", "achieved": round(r["tflops_kernel"], 2), "peak": PEAK_BF16_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(mfma_frac, 4)}
+    traffic, traffic_prov = measured_traffic(kernel_name)
     line = {
         "metric": METRIC,
         "value": round(r["tflops_step"], 2),
@@ -1242,7 +1266,7 @@ def main() -> None:
         "config": {"workload": "LLaDA-8B dense denoise-step attention: 32 layers x 8 sequences x 384 tokens "
                                "(prompt 256 + gen 128), 32 heads x 128, non-causal varlen",
                    "global_batch": 8, "seq_len": 384, "layers": n_layers},
-        "roofline": dict(roof, traffic=measured_traffic(kernel_name), kernel=kernel_name,
+        "roofline": dict(roof, traffic=traffic, traffic_recorded_on=traffic_prov, kernel=kernel_name,
                          kernel_us=round(r["kernel_us"], 3), flops_per_launch=r["flops_per_call"],
                          algorithmic_bytes_per_launch=r["bytes_per_call"],
                          arithmetic_intensity=round(intensity, 1), machine_balance=round(balance, 1),

@@ -47,7 +47,6 @@ struct AttnArgs {
   const int32_t* slots;
   const int32_t* slot_off;
   float* ws;          // split partials (K3b, n_split > 1)
-  int max_pages;      // K3b paged form: row stride of the page table (its rows come in `slots`)
   int64_t q_stride, k_stride, v_stride, o_stride;
   int64_t cache_slots;
   int n_seg, Hkv, g, mtiles, n_split, keys_per_split;
@@ -734,13 +733,18 @@ template <int RB, bool PAGED>
 // The launch geometry and the tables the first, dependent loads read come as
 // leading scalar arguments (14 dwords): the library is built with kernel
 // argument preloading, so they are in SGPRs when a wave starts instead of one
-// scalar load away (the rest of AttnArgs is loaded as usual).
+// scalar load away (the rest of AttnArgs is loaded as usual).  `slots` is
+// null when there is no cache.  `chunk_pages` = XCD chunk (1..16) + 32 x the
+// page table's row length (0 in the slot-list form), so that everything the
+// page-id fetch needs is preloaded.
 __global__ __launch_bounds__(256 * RB) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_cached_kernel(
     const int32_t* __restrict__ slot_off, const int32_t* __restrict__ seg_ids, const int32_t* __restrict__ cu_q,
-    const int32_t* __restrict__ slots, int xcd_chunk, int logical_blocks, int mtiles, int n_split, int Hkv,
+    const int32_t* __restrict__ slots, int chunk_pages, int logical_blocks, int mtiles, int n_split, int Hkv,
     int keys_per_split, AttnArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   constexpr int NJ = 8 / RB;  // K (and V) DMA instructions per wavefront per tile
+  const int xcd_chunk = chunk_pages & 31;
+  const int max_pages = chunk_pages >> 5;
   const int L = xcd_remap(blockIdx.x, xcd_chunk);
   if (L >= logical_blocks) return;
   const int mblocks = (mtiles + RB - 1) / RB;
@@ -751,26 +755,44 @@ __global__ __launch_bounds__(256 * RB) __attribute__((amdgpu_waves_per_eu(2, 2))
   r /= mblocks;
   const int hkv = r % Hkv;
   const int s = r / Hkv;
+  const int kbeg0 = split * keys_per_split;  // this split's first key (past Lk: no tiles)
+  const int tid = threadIdx.x;
+  const int wave_id = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  uint32_t* slot_ring = reinterpret_cast<uint32_t*>(lds + 2 * CK_STAGE);  // [4 tiles][4 RB waves][64]
+  // Page-table form: each wavefront's page ids (pg0 .. pg0 + 63 of the
+  // segment's row, one per lane; ids past the row read a valid dummy) sit in
+  // the upper half of the ring -- the merge at the end parks every row
+  // block's m / l in its first 256 RB words while other wavefronts may still
+  // read page ids for their last tiles.  Their address needs no load, so the
+  // fetch is the kernel's first memory operation and the segment's offsets
+  // are loaded behind it.
+  const int pg0 = kbeg0 >> 8;
+  uint32_t* const page_ring = slot_ring + 512 * RB + wave_id * 64;
+  if constexpr (PAGED) {
+    if (slots != nullptr && max_pages > 0) {  // else no row has a page: nothing to fetch
+      const int32_t* row = slots + (int64_t)s * max_pages;
+      const int idx = pg0 + lane;
+      __builtin_amdgcn_global_load_lds(idx < max_pages ? row + idx : row,
+                                       (__attribute__((address_space(3))) void*)page_ring, 4, 0, 0);
+    }
+  }
   // The slot list of segment s needs slot_off only: its first fetches are
   // issued before the segment's rows (cu_q, possibly behind seg_ids) are
   // known, so that those two dependent loads overlap.
-  // (The scalar loads of the segment's offsets all come first: a load after
-  // the first DMA into LDS could no longer be a scalar one.)
+  // (In the slot-list form the scalar loads of the segment's offsets come
+  // first: a load after the first DMA into LDS can no longer be a scalar one.)
   const int slot_base = PAGED ? 0 : slot_off[s];
   const int n_c = PAGED ? max(slot_off[s], 0) : slot_off[s + 1] - slot_base;
-  const int kbeg0 = split * keys_per_split;  // this split's first key (past Lk: no tiles)
   const int sid = seg_ids ? seg_ids[s] : s;
   const int qrow0 = cu_q[sid];
   const int Lq = cu_q[sid + 1] - qrow0;
 
-  const int tid = threadIdx.x;
-  const int wave_id = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wave = wave_id & 3;     // key block of the tile
   const int rblk = wave_id >> 2;    // row block
   const int mt = mb * RB + rblk;
   const int m_base = mt * 32;
   const int jb = rblk * NJ;         // first DMA instruction of this wavefront
-  const int lane = tid & 63;
   const int lrow = lane & 31;
   const int hl = lane >> 5;
   const int rl = lane >> 4, P = lane & 15;
@@ -782,11 +804,8 @@ __global__ __launch_bounds__(256 * RB) __attribute__((amdgpu_waves_per_eu(2, 2))
   const int64_t row_elems = (int64_t)Hkv * HD;
   // without a cache (cache_slots = 0, slots may be null) every cached row is
   // outside it: the fetches then read slot_off[0], a valid dummy
-  const bool have_slots = n_c > 0 && slots != nullptr && a.cache_slots > 0 && (!PAGED || a.max_pages > 0);
-  const int32_t* sp = have_slots ? slots + (PAGED ? (int64_t)s * a.max_pages : (int64_t)slot_base) : slot_off;
-  // paged: page ids [pg0, pg0 + 256 RB) of the segment's row, one per lane of
-  // every wavefront, in the ring (ids past the row read a valid dummy)
-  const int pg0 = kbeg0 >> 8;
+  const bool have_slots = n_c > 0 && slots != nullptr && (!PAGED || max_pages > 0);
+  const int32_t* sp = have_slots && !PAGED ? slots + slot_base : slot_off;
   // Per-wave pipeline: the slots of tile t+2 are fetched before tile t+1's
   // DMA is issued, so that after computing tile t the wave can issue tile
   // t+2 into the stage it just freed while tile t+1 is still in flight --
@@ -797,21 +816,11 @@ __global__ __launch_bounds__(256 * RB) __attribute__((amdgpu_waves_per_eu(2, 2))
   // tile) into a ring of four per-wave entries behind the stages, and lanes
   // read them from LDS after the wait that retires the fetch: no register is
   // ever written by a load the compiler does not know about.
-  uint32_t* slot_ring = reinterpret_cast<uint32_t*>(lds + 2 * CK_STAGE);  // [4 tiles][4 RB waves][64]
   auto fetch_slots = [&](int t) {
     const int kidx = kbeg0 + t * CK_TILE + 32 * wave + lrow;
     const int32_t* src = have_slots ? sp + min(max(kidx, 0), n_c - 1) : sp;
     __builtin_amdgcn_global_load_lds(
         src, (__attribute__((address_space(3))) void*)(slot_ring + ((t & 3) * 4 * RB + wave_id) * 64), 4, 0, 0);
-  };
-  // Each wavefront's page ids sit in the upper half of the ring: the merge at
-  // the end parks every row block's m / l in its first 256 RB words while
-  // other wavefronts may still read page ids for their last tiles.
-  uint32_t* const page_ring = slot_ring + 512 * RB + wave_id * 64;
-  auto fetch_pages = [&]() {
-    const int idx = pg0 + lane;
-    const int32_t* src = have_slots && idx < a.max_pages ? sp + idx : (have_slots ? sp : slot_off);
-    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)page_ring, 4, 0, 0);
   };
   // After the prologue's wait lane l holds page id pg0 + l in a register, and
   // the page of a tile (the same for the whole wavefront) is one lane read.
@@ -822,7 +831,7 @@ __global__ __launch_bounds__(256 * RB) __attribute__((amdgpu_waves_per_eu(2, 2))
   auto page_of = [&](int t) -> int {
     const int pg = (kbeg0 + t * CK_TILE) >> 8;
     const int pid = __builtin_amdgcn_readlane(page_reg, (pg - pg0) & 63);
-    return have_slots && pg < a.max_pages && (uint32_t)pid < n_pages ? pid * 256 : -1;
+    return have_slots && pg < max_pages && (uint32_t)pid < n_pages ? pid * 256 : -1;
   };
   // this lane's slots of tile t (rows 4 (jb + j) + rl of the wave's 32); call after the wait
   auto read_slots = [&](int t, int (&dst)[NJ]) {
@@ -840,15 +849,14 @@ __global__ __launch_bounds__(256 * RB) __attribute__((amdgpu_waves_per_eu(2, 2))
       for (int j = 0; j < NJ; ++j) dst[j] = (int)e[4 * (jb + j) + rl];
     }
   };
-  // ---- prologue: the slots of the first three tiles, then the Q^T
-  // fragments (their address needs the segment's rows); D(0) and D(1) are
-  // issued as soon as the slots have landed, with q still in flight, and a
-  // wait that retires q follows them (so the compiler's own wait tracking
-  // has no q load left to wait for inside the tile loop).  Slot fetches
-  // past the key range read a clamped, valid index and go unused.
-  if constexpr (PAGED) {
-    fetch_pages();
-  } else {
+  // ---- prologue: the slots of the first three tiles (the page ids went
+  // out at the start), then the Q^T fragments (their address needs the
+  // segment's rows); D(0) and D(1) are issued as soon as the slots have
+  // landed, with q still in flight, and a wait that retires q follows them
+  // (so the compiler's own wait tracking has no q load left to wait for
+  // inside the tile loop).  Slot fetches past the key range read a clamped,
+  // valid index and go unused.
+  if constexpr (!PAGED) {
     fetch_slots(0);
     fetch_slots(1);
     fetch_slots(2);
@@ -1265,7 +1273,7 @@ static int block_cached_impl(const char* name, const dllm_bf16* q, const dllm_bf
   if (paged && (max_pages < 0 || (cache_slots > 0 && max_pages == 0) || cache_slots % 256))
     return fail(DLLM_ERR_INVALID_ARG, "%s: max_pages %d, cache rows %lld: the cache must be whole 256-row pages",
                 name, max_pages, (long long)cache_slots);
-  if (paged && (int64_t)n_seg * max_pages >= ((int64_t)1 << 31))
+  if (paged && ((int64_t)n_seg * max_pages >= ((int64_t)1 << 31) || max_pages >= (1 << 26)))
     return fail(DLLM_ERR_INVALID_ARG, "%s: page table too large", name);
   if (cache_slots > 0 && (!aligned16(k_cache) || !aligned16(v_cache)))
     return fail(DLLM_ERR_INVALID_ARG, "%s: caches must be 16-byte aligned", name);
@@ -1275,7 +1283,6 @@ static int block_cached_impl(const char* name, const dllm_bf16* q, const dllm_bf
   a.cu_q = cu; a.cu_k = cu; a.seg_ids = seg_ids; a.slots = slots; a.slot_off = slot_off;
   a.q_stride = q_stride_tok; a.k_stride = k_stride_tok; a.v_stride = v_stride_tok; a.o_stride = o_stride_tok;
   a.n_seg = n_seg; a.Hkv = Hkv; a.g = Hq / Hkv;
-  a.max_pages = paged ? max_pages : 0;
   int mtiles, rb, n_split, kps;
   block_cached_plan(n_seg, max_q, max_keys, Hq, Hkv, mtiles, rb, n_split, kps);
   a.mtiles = mtiles; a.n_split = n_split; a.keys_per_split = kps;
@@ -1302,8 +1309,12 @@ static int block_cached_impl(const char* name, const dllm_bf16* q, const dllm_bf
   auto launch = [&](auto kern, int threads, int lds_bytes) -> int {
     int r = set_lds(kern, lds_bytes, name);
     if (r) return r;
-    kern<<<dim3(nb), dim3(threads), lds_bytes, st>>>(a.slot_off, a.seg_ids, a.cu_q, a.slots, a.xcd_chunk,
-                                                      a.logical_blocks, a.mtiles, a.n_split, a.Hkv, a.keys_per_split, a);
+    // no cache: no slot list or page table to read (the kernels test for null)
+    const int32_t* table = cache_slots > 0 ? a.slots : nullptr;
+    const int chunk_pages = a.xcd_chunk + 32 * (paged ? max_pages : 0);
+    kern<<<dim3(nb), dim3(threads), lds_bytes, st>>>(a.slot_off, a.seg_ids, a.cu_q, table, chunk_pages,
+                                                      a.logical_blocks, a.mtiles, a.n_split, a.Hkv, a.keys_per_split,
+                                                      a);
     return DLLM_OK;
   };
   if (rb == 2)

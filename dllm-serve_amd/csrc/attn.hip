@@ -1270,9 +1270,12 @@ static int block_cached_impl(const char* name, const dllm_bf16* q, const dllm_bf
     return fail(DLLM_ERR_UNSUPPORTED, "%s: k / v token strides must be below 4 GiB", name);
   if (cache_slots > 0 && (!k_cache || !v_cache || !slots))
     return fail(DLLM_ERR_INVALID_ARG, "%s: null cache / %s", name, paged ? "page table" : "slots");
-  if (paged && (max_pages < 0 || (cache_slots > 0 && max_pages == 0) || cache_slots % 256))
-    return fail(DLLM_ERR_INVALID_ARG, "%s: max_pages %d, cache rows %lld: the cache must be whole 256-row pages",
-                name, max_pages, (long long)cache_slots);
+  if (paged && (max_pages < 0 || (cache_slots > 0 && max_pages == 0)))
+    return fail(DLLM_ERR_INVALID_ARG, "%s: max_pages %d: a page table with a cache needs at least one page per row",
+                name, max_pages);
+  if (paged && cache_slots % 256)
+    return fail(DLLM_ERR_INVALID_ARG, "%s: cache rows %lld: the cache must be whole 256-row pages", name,
+                (long long)cache_slots);
   if (paged && ((int64_t)n_seg * max_pages >= ((int64_t)1 << 31) || max_pages >= (1 << 26)))
     return fail(DLLM_ERR_INVALID_ARG, "%s: page table too large", name);
   if (cache_slots > 0 && (!aligned16(k_cache) || !aligned16(v_cache)))

@@ -87,6 +87,42 @@ def test_argument_validation_without_gpu():
     assert lib.dllm_store_kvcache(None, 4096, None, 4096, None, None, 10, None, 0, 4096, None) == 0
 
 
+def test_paged_block_cached_validation_without_gpu():
+    """The page-table form rejects what it cannot address before any launch:
+    a cache that is not whole 256-row pages, a missing page table or cached
+    lengths, a page-table row length that the launch cannot carry, and a
+    missing workspace when the keys are split."""
+    lib = _capi.load()
+    P = ctypes.c_void_p
+    fake = P(4096)
+
+    def call(num_pages=16, pt=fake, max_pages=4, clen=fake, n_seg=2, max_keys=96, ws=None, ws_bytes=0,
+             kc=fake, vc=fake):
+        return _err(lib.dllm_attn_block_cached_paged_fwd(fake, fake, fake, fake, fake, None, n_seg, 32, max_keys,
+                                                         kc, vc, num_pages, pt, max_pages, clen, 32, 32, 128,
+                                                         4096, 4096, 4096, 4096, 0.1, ws, ws_bytes, None))
+
+    rc, msg = call(num_pages=-1)
+    assert rc == _capi.DLLM_ERR_INVALID_ARG and "num_pages" in msg
+    rc, msg = call(clen=None)
+    assert rc == _capi.DLLM_ERR_INVALID_ARG and "cached_len" in msg
+    rc, msg = call(pt=None)
+    assert rc == _capi.DLLM_ERR_INVALID_ARG and "page table" in msg
+    rc, msg = call(max_pages=0)
+    assert rc == _capi.DLLM_ERR_INVALID_ARG and "max_pages" in msg
+    rc, msg = call(max_pages=1 << 26)
+    assert rc == _capi.DLLM_ERR_INVALID_ARG and "page table too large" in msg
+    rc, msg = call(kc=None)
+    assert rc == _capi.DLLM_ERR_INVALID_ARG
+    # two 32-row blocks against 4096 cached rows: split over the keys, a workspace is needed
+    need = _capi.block_cached_workspace_size(2, 32, 4128, 32, 32, 128)
+    assert need > 0
+    rc, msg = call(max_keys=4128, max_pages=16)
+    assert rc == _capi.DLLM_ERR_WORKSPACE
+    # nothing to do: no segments
+    assert call(n_seg=0)[0] == 0
+
+
 def test_missing_library_fails_loudly(tmp_path, monkeypatch):
     monkeypatch.setattr(_capi, "_lib", None)
     with pytest.raises(RuntimeError, match="no CPU fallback"):

@@ -726,9 +726,10 @@ __device__ __forceinline__ void cached_tile(const uint8_t* Ks, const uint8_t* Vs
 // the page table ([n_seg][max_pages] int32 page ids, 256-row pages): cached
 // row r sits in cache row page_table[s][r / 256] * 256 + r % 256.  A 128-key
 // tile starts at a multiple of 128, so its cached rows lie in one page.  Each
-// wavefront DMAs its own copy of the page ids of its key range (up to 64) at
-// the start, next to Q -- no wavefront waits for another -- so its first K/V
-// tiles wait on one load instead of two (slot offsets, then the slot list).
+// wavefront DMAs its own copy of the page ids of its key range (up to 64) as
+// its first memory operation -- no wavefront waits for another -- so its first
+// K/V tiles wait on one round of loads (page ids, offsets and Q together)
+// instead of two (slot offsets, then the slot list).
 template <int RB, bool PAGED>
 // The launch geometry and the tables the first, dependent loads read come as
 // leading scalar arguments (14 dwords): the library is built with kernel
@@ -761,7 +762,7 @@ __global__ __launch_bounds__(256 * RB) __attribute__((amdgpu_waves_per_eu(2, 2))
   const int lane = tid & 63;
   uint32_t* slot_ring = reinterpret_cast<uint32_t*>(lds + 2 * CK_STAGE);  // [4 tiles][4 RB waves][64]
   // Page-table form: each wavefront's page ids (pg0 .. pg0 + 63 of the
-  // segment's row, one per lane; ids past the row read a valid dummy) sit in
+  // segment's row, one per lane; lanes past the row's end read its first id) sit in
   // the upper half of the ring -- the merge at the end parks every row
   // block's m / l in its first 256 RB words while other wavefronts may still
   // read page ids for their last tiles.  Their address needs no load, so the
@@ -780,8 +781,9 @@ __global__ __launch_bounds__(256 * RB) __attribute__((amdgpu_waves_per_eu(2, 2))
   // The slot list of segment s needs slot_off only: its first fetches are
   // issued before the segment's rows (cu_q, possibly behind seg_ids) are
   // known, so that those two dependent loads overlap.
-  // (In the slot-list form the scalar loads of the segment's offsets come
-  // first: a load after the first DMA into LDS can no longer be a scalar one.)
+  // (A load of memory that an earlier DMA into LDS also reads -- the slot
+  // fetches read slot_off as their dummy -- can no longer be a scalar load,
+  // so in the slot-list form the offsets are loaded first.)
   const int slot_base = PAGED ? 0 : slot_off[s];
   const int n_c = PAGED ? max(slot_off[s], 0) : slot_off[s + 1] - slot_base;
   const int sid = seg_ids ? seg_ids[s] : s;

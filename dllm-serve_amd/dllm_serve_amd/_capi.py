@@ -254,6 +254,14 @@ def attn_block_cached_paged_fwd(q, k, v, o, cu, seg_ids, n_seg, max_q, max_keys,
     """K3b, page-table form: segment s's cached rows are rows r < cached_len[s]
     of its pages page_table[s, r // 256] (256-row pages of the cache, given
     as [num_pages, 256, Hkv, D] or flat rows)."""
+    # the kernel reads int32 rows of the table (one per launch segment) and int32 lengths
+    if page_table.dtype != torch.int32 or page_table.dim() != 2 or page_table.stride(1) != 1 \
+            or page_table.stride(0) != page_table.shape[1] or page_table.shape[0] < n_seg:
+        raise ValueError("page_table must be a contiguous int32 [n_seg, max_pages] tensor, one row per launch "
+                         f"segment; got {tuple(page_table.shape)} {page_table.dtype}")
+    if cached_len.dtype != torch.int32 or not cached_len.is_contiguous() or cached_len.numel() < n_seg:
+        raise ValueError(f"cached_len must be a contiguous int32 tensor of n_seg = {n_seg} lengths; "
+                         f"got {tuple(cached_len.shape)} {cached_len.dtype}")
     _require_gpu(q, k, v, o, cu, page_table, cached_len)
     lib = load()
     Hkv, D = k.shape[1], k.shape[2]
@@ -264,7 +272,7 @@ def attn_block_cached_paged_fwd(q, k, v, o, cu, seg_ids, n_seg, max_q, max_keys,
     rc = lib.dllm_attn_block_cached_paged_fwd(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), cu.data_ptr(), _ptr(seg_ids), n_seg, max_q,
         max_keys, _ptr(k_cache) if num_pages else None, _ptr(v_cache) if num_pages else None, num_pages,
-        page_table.data_ptr(), page_table.shape[1] if page_table.dim() == 2 else page_table.numel() // max(n_seg, 1),
+        page_table.data_ptr(), page_table.shape[1],
         cached_len.data_ptr(), q.shape[1], Hkv, D, q.stride(0), k.stride(0), v.stride(0), o.stride(0), float(scale),
         _ptr(workspace), ws_bytes, _stream(q.device))
     _check(rc, "dllm_attn_block_cached_paged_fwd")

@@ -123,6 +123,27 @@ def test_paged_block_cached_validation_without_gpu():
     assert call(n_seg=0)[0] == 0
 
 
+def test_paged_wrapper_checks_table_and_lengths():
+    """The Python wrapper refuses a page table or lengths the kernel would
+    misread (wrong dtype, not one contiguous row per segment, too few rows)."""
+    import torch
+    q = k = v = o = torch.zeros(4, 2, 128, dtype=torch.bfloat16)
+    cu = torch.tensor([0, 2, 4], dtype=torch.int32)
+    good_pt = torch.zeros(2, 3, dtype=torch.int32)
+    good_len = torch.zeros(2, dtype=torch.int32)
+    bad_tables = [torch.zeros(2, 3, dtype=torch.int64), torch.zeros(6, dtype=torch.int32),
+                  torch.zeros(3, 2, dtype=torch.int32).t(), torch.zeros(1, 3, dtype=torch.int32)]
+    for pt in bad_tables:
+        with pytest.raises(ValueError, match="page_table"):
+            _capi.attn_block_cached_paged_fwd(q, k, v, o, cu, None, 2, 2, 6, None, None, pt, good_len, 0.1, None)
+    for ln in (torch.zeros(2, dtype=torch.int64), torch.zeros(1, dtype=torch.int32)):
+        with pytest.raises(ValueError, match="cached_len"):
+            _capi.attn_block_cached_paged_fwd(q, k, v, o, cu, None, 2, 2, 6, None, None, good_pt, ln, 0.1, None)
+    # well-formed arguments get as far as the GPU check
+    with pytest.raises(RuntimeError, match="GPU only"):
+        _capi.attn_block_cached_paged_fwd(q, k, v, o, cu, None, 2, 2, 6, None, None, good_pt, good_len, 0.1, None)
+
+
 def test_missing_library_fails_loudly(tmp_path, monkeypatch):
     monkeypatch.setattr(_capi, "_lib", None)
     with pytest.raises(RuntimeError, match="no CPU fallback"):
